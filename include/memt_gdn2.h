@@ -1,0 +1,180 @@
+/*
+ * memt_gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 native-memory hot path.
+ *
+ * Every entry point takes device pointers, plain sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream).  None allocates
+ * memory, none synchronises the host, and all are reentrant: each call only
+ * enqueues kernels on `stream`.  Tensors are token-major and contiguous,
+ * exactly as in the reference ([B=1, T, H, D] with the packed token axis
+ * first, states [N, H, K, V] fp32).  bf16 is passed as its 16-bit storage.
+ *
+ * Status: 0 on success, a negative MEMT_GDN2_E* code otherwise
+ * (memt_gdn2_strerror names it).  Arguments are validated on the host; a
+ * plan (chunk table) is trusted as built by the caller: chunk_len in 1..64,
+ * chunk_tok0 + chunk_len within the token axis, offsets non-decreasing.
+ */
+#ifndef MEMT_GDN2_H
+#define MEMT_GDN2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MEMT_GDN2_ABI_VERSION 1
+
+#define MEMT_GDN2_OK 0
+#define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
+#define MEMT_GDN2_EUNSUPPORTED (-2) /* head dim / dtype without a compiled variant */
+#define MEMT_GDN2_ELAUNCH (-3)      /* the HIP launch reported an error */
+#define MEMT_GDN2_EWORKSPACE (-4)   /* workspace missing or too small */
+
+/* element types */
+#define MEMT_GDN2_F32 0
+#define MEMT_GDN2_BF16 1
+
+/* output gate of the readout epilogue */
+#define MEMT_GDN2_GATE_SOFTCAP_SILU 0 /* c * tanh(silu(g) / c): MemTRMSNormGated */
+#define MEMT_GDN2_GATE_SIGMOID 1      /* sigmoid(g) */
+
+/* what the chunked update writes to `o` */
+#define MEMT_GDN2_OUT_NONE 0     /* state only */
+#define MEMT_GDN2_OUT_SNAPSHOT 1 /* o_t = scale * q_t^T bf16(read_states[seq(t)]) (MemT commit) */
+#define MEMT_GDN2_OUT_CAUSAL 2   /* o_t = scale * q_t^T S_t (state after token t) */
+
+/* chunk-plan flag bits */
+#define MEMT_GDN2_CHUNK_BLOCK_START 1 /* store a snapshot before this chunk */
+#define MEMT_GDN2_CHUNK_COMMIT 2      /* apply this chunk's update */
+
+/*
+ * Chunk table: the device-side part of the reference's ChunkPlan
+ * (models/qwen/ops/layout.py:18-44).  Chunks are at most 64 tokens and never
+ * cross a write event; the decay cumsum restarts at every chunk start.
+ */
+typedef struct memt_gdn2_plan {
+  const int32_t* chunk_tok0;        /* [n_chunk] first token of the chunk on the packed axis */
+  const int32_t* chunk_len;         /* [n_chunk] tokens in the chunk, 1..64 */
+  const int32_t* seq_chunk_offsets; /* [n_seq + 1] chunk range of each sequence/sample */
+  const int32_t* chunk_block_ids;   /* [n_chunk] snapshot (read block) of each chunk, or NULL */
+  const int32_t* chunk_flags;       /* [n_chunk] MEMT_GDN2_CHUNK_* bits, or NULL (= commit, no snapshot) */
+  int32_t n_chunk;
+  int32_t n_seq;
+  int32_t n_block; /* rows of `snaps` */
+  int32_t reserved;
+} memt_gdn2_plan;
+
+int memt_gdn2_abi_version(void);
+const char* memt_gdn2_strerror(int status);
+
+/*
+ * Row L2 normalisation y = x / sqrt(sum(x^2) + eps), rstd = 1/sqrt(...).
+ * Replaces FLA l2norm_fwd (_vendor/fla/modules/l2norm.py:147-197); dim <= 512.
+ * x_dtype/y_dtype: MEMT_GDN2_BF16 or MEMT_GDN2_F32; rstd may be NULL.
+ */
+int memt_gdn2_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd,
+                         int64_t rows, int dim, float eps, void* stream);
+
+/*
+ * Chunk-local cumulative sum of g [tokens, H, S] over each plan chunk,
+ * times `scale` (log2 units when scale = 1/ln 2), fp32 out; `reverse` sums
+ * from the chunk end.  Replaces chunk_local_cumsum / chunk_local_cumsum_vector
+ * (_vendor/fla/ops/utils/cumsum.py:299-338,444-480) for the [B,T,H,S] layout.
+ */
+int memt_gdn2_chunk_local_cumsum(const void* g, int g_dtype, float* gk, const memt_gdn2_plan* plan,
+                                 int H, int S, float scale, int reverse, void* stream);
+
+/*
+ * Bytes of device workspace memt_gdn2_chunk_update needs for this plan.
+ */
+size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int H, int K, int V, int out_mode);
+
+/*
+ * The chunked GDN-2 memory update (stable gated delta rule) end to end:
+ * chunk-local decay cumsum, WY/UT transform, inter-chunk fp32 state
+ * recurrence and the chosen output.  Replaces token_memory_packed
+ * (models/qwen/ops/packed.py:34-81; Flash: models/deepseek/ops/packed.py:70-108)
+ * when out_mode = SNAPSHOT, and the FLA chunk GDN-2 forward when CAUSAL.
+ *
+ *   q, k     [T, H, K] bf16 (q may be NULL when out_mode = NONE)
+ *   v        [T, H, V] bf16
+ *   g        [T, H, K] fp32 natural-log decay (<= 0)
+ *   beta     [T, H, V] write gate, beta_dtype F32 or BF16
+ *   b        [T, H, K] bf16 channel erase gate, or NULL for b = 1
+ *   h0       [n_seq, H, K, V] fp32 initial states (write_states), or NULL for 0
+ *   ht       [n_seq, H, K, V] fp32 final states, or NULL
+ *   read_states [n_block, H, K, V] fp32, used by out_mode = SNAPSHOT
+ *   snaps    [n_block, H, K, V] fp32 state before each block-start chunk, or NULL
+ *   o        [T, H, V] bf16 output (out_mode != NONE)
+ * K, V in {64, 128, 256}.  The workspace must hold
+ * memt_gdn2_chunk_update_workspace_size(...) bytes, 256-byte aligned.
+ */
+int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g,
+                           const void* beta, int beta_dtype, const void* b, const float* h0,
+                           float* ht, const float* read_states, float* snaps, void* o,
+                           const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale,
+                           int out_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * WY stage only (replaces chunk_gdn2_fwd_intra, _vendor/fla/ops/gdn2/chunk_intra.py:693-787),
+ * writing the reference layouts: w, kg [T,H,K] bf16, u [T,H,V] bf16, Akk [T,H,64] bf16
+ * (the inverse (I+L)^-1), Aqk [T,H,64] bf16 (scale included; needs q), qg [T,H,K] bf16
+ * (q * 2^gk, optional).  gk is the chunk-local cumulative decay in log2 units.
+ * Any output pointer may be NULL.  Uses the same workspace as memt_gdn2_chunk_update
+ * with out_mode = CAUSAL when q is given, else NONE.
+ */
+int memt_gdn2_wy_fwd(const void* q, const void* k, const void* v, const float* gk, const void* b,
+                     const void* beta, int beta_dtype, const memt_gdn2_plan* plan, int64_t T, int H,
+                     int K, int V, float scale, void* w, void* u, void* kg, void* Akk, void* Aqk,
+                     void* qg, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Inter-chunk state scan from reference-layout WY tensors (replaces
+ * memt_gdn2_fwd_h, models/qwen/ops/_triton/state.py:127-174):
+ *   kg, w [T,H,K] bf16, u [T,H,V] bf16, gk [T,H,K] fp32 (log2 cumsum),
+ *   h0 [n_seq,H,K,V] or NULL, snaps [n_block,H,K,V] or NULL, ht [n_seq,H,K,V] or NULL.
+ * Snapshots are stored before every chunk flagged BLOCK_START; chunks without
+ * COMMIT leave the state unchanged.  Uses the chunk_update workspace (out_mode NONE).
+ */
+int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* gk,
+                    const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, const float* h0,
+                    float* snaps, float* ht, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Snapshot reader: o[t] = bf16(scale * q[t]^T bf16(snaps[block(chunk(t))])), fp32
+ * accumulation.  Replaces memt_gdn2_read_fwd (models/qwen/ops/read.py:10-39,
+ * models/qwen/ops/_triton/read.py:22-71).  q [T,H,K] bf16, snaps [n_block,H,K,V] fp32,
+ * o [T,H,V] bf16; plan.chunk_block_ids required.
+ */
+int memt_gdn2_read_fwd(const void* q, const float* snaps, void* o, const memt_gdn2_plan* plan,
+                       int64_t T, int H, int K, int V, float scale, void* stream);
+
+/*
+ * MemTRMSNormGated (models/qwen/layer.py:15-31): for each row of x [rows, dim] bf16,
+ * y = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * w); out = bf16(y * gate_fn(gate)),
+ * gate_fn = softcap * tanh(silu(.) / softcap) or sigmoid.  gate [rows, dim] bf16,
+ * weight [dim] bf16, dim <= 1024.
+ */
+int memt_gdn2_rms_norm_gated(const void* x, const void* gate, const void* weight, void* out,
+                             int64_t rows, int dim, float eps, float softcap, int gate_kind,
+                             void* stream);
+
+/*
+ * Fused decode readout: for each sequence b and head h,
+ *   r   = bf16(scale * q[b,h]^T S[slot(b),h])       (fp32 state, fp32 accumulation)
+ *   out = MemTRMSNormGated(r, gate[b,h]) as above   ([B, H*V] bf16)
+ * S [slots, H, K, V] fp32; slot_idx [B] int32 or NULL (slot = b); q [B,H,K] bf16;
+ * gate [B,H,V] bf16; weight [V] bf16.  Replaces the query path of
+ * QwenMemoryBlock.packed (models/qwen/layer.py:112-131): memt_gdn2_read_fwd + o_norm.
+ */
+int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void* q,
+                            const void* gate, const void* weight, void* out, int B, int H, int K,
+                            int V, float scale, float eps, float softcap, int gate_kind,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEMT_GDN2_H */

@@ -1,0 +1,232 @@
+// extern "C" entry points of libmemt_gdn2.so (declared in include/memt_gdn2.h).
+// Host-side argument checks, workspace carving and kernel dispatch.  No entry
+// point allocates memory or synchronises the host.
+#include "gdn2_internal.h"
+
+using namespace memt;
+
+namespace {
+
+bool supported_kv(int K, int V) { return (K == 64 && V == 64) || (K == 128 && V == 128); }
+
+int status_of(hipError_t e) { return e == hipSuccess ? MEMT_GDN2_OK : MEMT_GDN2_ELAUNCH; }
+
+bool plan_ok(const memt_gdn2_plan* p) {
+  return p != nullptr && p->n_chunk >= 0 && p->n_seq >= 0 &&
+         (p->n_chunk == 0 || (p->chunk_tok0 != nullptr && p->chunk_len != nullptr));
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int memt_gdn2_abi_version(void) { return MEMT_GDN2_ABI_VERSION; }
+
+const char* memt_gdn2_strerror(int status) {
+  switch (status) {
+    case MEMT_GDN2_OK: return "ok";
+    case MEMT_GDN2_EINVAL: return "invalid argument (null pointer or inconsistent sizes)";
+    case MEMT_GDN2_EUNSUPPORTED: return "unsupported head dimension or dtype";
+    case MEMT_GDN2_ELAUNCH: return "kernel launch failed";
+    case MEMT_GDN2_EWORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+int memt_gdn2_l2norm_fwd(const void* x, int x_dtype, void* y, int y_dtype, float* rstd, int64_t rows, int dim,
+                         float eps, void* stream) {
+  if (rows < 0 || dim <= 0) return MEMT_GDN2_EINVAL;
+  if (rows > 0 && (x == nullptr || y == nullptr)) return MEMT_GDN2_EINVAL;
+  if (dim > 512) return MEMT_GDN2_EUNSUPPORTED;
+  if ((x_dtype != MEMT_GDN2_BF16 && x_dtype != MEMT_GDN2_F32) ||
+      (y_dtype != MEMT_GDN2_BF16 && y_dtype != MEMT_GDN2_F32))
+    return MEMT_GDN2_EUNSUPPORTED;
+  return status_of(launch_l2norm(x, x_dtype == MEMT_GDN2_BF16, y, y_dtype == MEMT_GDN2_BF16, rstd, rows, dim, eps,
+                                 (hipStream_t)stream));
+}
+
+int memt_gdn2_chunk_local_cumsum(const void* g, int g_dtype, float* gk, const memt_gdn2_plan* plan, int H, int S,
+                                 float scale, int reverse, void* stream) {
+  if (!plan_ok(plan) || H <= 0 || S <= 0) return MEMT_GDN2_EINVAL;
+  if (plan->n_chunk > 0 && (g == nullptr || gk == nullptr)) return MEMT_GDN2_EINVAL;
+  if (g_dtype != MEMT_GDN2_BF16 && g_dtype != MEMT_GDN2_F32) return MEMT_GDN2_EUNSUPPORTED;
+  return status_of(launch_cumsum(g, g_dtype == MEMT_GDN2_BF16, gk, plan->chunk_tok0, plan->chunk_len, plan->n_chunk,
+                                 H, S, scale, reverse != 0, (hipStream_t)stream));
+}
+
+size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int H, int K, int V, int out_mode) {
+  if (n_chunk < 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+  return wy_layout(n_chunk, H, K, V, out_mode == MEMT_GDN2_OUT_CAUSAL).total;
+}
+
+int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                           int beta_dtype, const void* b, const float* h0, float* ht, const float* read_states,
+                           float* snaps, void* o, const memt_gdn2_plan* plan, int64_t T, int H, int K, int V,
+                           float scale, int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
+  if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
+  if (out_mode != MEMT_GDN2_OUT_NONE && out_mode != MEMT_GDN2_OUT_SNAPSHOT && out_mode != MEMT_GDN2_OUT_CAUSAL)
+    return MEMT_GDN2_EINVAL;
+  if (plan->n_chunk > 0) {
+    if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || plan->seq_chunk_offsets == nullptr)
+      return MEMT_GDN2_EINVAL;
+    if (!aligned16(k) || !aligned16(v) || (b && !aligned16(b)) || (q && !aligned16(q))) return MEMT_GDN2_EINVAL;
+    if (out_mode != MEMT_GDN2_OUT_NONE && (q == nullptr || o == nullptr)) return MEMT_GDN2_EINVAL;
+    if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && (read_states == nullptr || plan->chunk_block_ids == nullptr))
+      return MEMT_GDN2_EINVAL;
+    if (snaps != nullptr && (plan->chunk_flags == nullptr || plan->chunk_block_ids == nullptr))
+      return MEMT_GDN2_EINVAL;
+  }
+  const bool causal = out_mode == MEMT_GDN2_OUT_CAUSAL;
+  const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, causal);
+  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
+    return MEMT_GDN2_EWORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const WyBuffers buf = wy_buffers(workspace, lay, causal);
+
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT) {
+    hipError_t e = launch_read_fwd((const __bf16*)q, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
+                                   plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st);
+    if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+  }
+  WyArgs wa{};
+  wa.q = causal ? (const __bf16*)q : nullptr;
+  wa.k = (const __bf16*)k;
+  wa.v = (const __bf16*)v;
+  wa.g = g;
+  wa.beta = beta;
+  wa.b = (const __bf16*)b;
+  wa.chunk_tok0 = plan->chunk_tok0;
+  wa.chunk_len = plan->chunk_len;
+  wa.H = H;
+  wa.scale = scale;
+  wa.out = buf;
+  wa.A_ref = nullptr;
+  hipError_t e = launch_wy(wa, plan->n_chunk, K, V, causal, false, beta_dtype == MEMT_GDN2_BF16, st);
+  if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+
+  StateArgs sa{};
+  sa.in = buf;
+  sa.chunk_tok0 = plan->chunk_tok0;
+  sa.chunk_len = plan->chunk_len;
+  sa.seq_chunk_offsets = plan->seq_chunk_offsets;
+  sa.chunk_block_ids = plan->chunk_block_ids;
+  sa.chunk_flags = plan->chunk_flags;
+  sa.h0 = h0;
+  sa.ht = ht;
+  sa.snaps = snaps;
+  sa.o = causal ? (__bf16*)o : nullptr;
+  sa.H = H;
+  sa.n_seq = plan->n_seq;
+  sa.scale = scale;
+  return status_of(launch_state(sa, K, V, causal, st));
+}
+
+int memt_gdn2_wy_fwd(const void* q, const void* k, const void* v, const float* gk, const void* b, const void* beta,
+                     int beta_dtype, const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale, void* w,
+                     void* u, void* kg, void* Akk, void* Aqk, void* qg, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
+  if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
+  if (plan->n_chunk > 0 && (k == nullptr || v == nullptr || gk == nullptr || beta == nullptr)) return MEMT_GDN2_EINVAL;
+  if ((Aqk != nullptr || qg != nullptr) && q == nullptr) return MEMT_GDN2_EINVAL;
+  const bool causal = q != nullptr;
+  const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, causal);
+  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
+    return MEMT_GDN2_EWORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const WyBuffers buf = wy_buffers(workspace, lay, causal);
+  WyArgs wa{};
+  wa.q = (const __bf16*)q;
+  wa.k = (const __bf16*)k;
+  wa.v = (const __bf16*)v;
+  wa.g = gk;
+  wa.beta = beta;
+  wa.b = (const __bf16*)b;
+  wa.chunk_tok0 = plan->chunk_tok0;
+  wa.chunk_len = plan->chunk_len;
+  wa.H = H;
+  wa.scale = scale;
+  wa.out = buf;
+  wa.A_ref = (__bf16*)Akk;
+  hipError_t e = launch_wy(wa, plan->n_chunk, K, V, causal, true, beta_dtype == MEMT_GDN2_BF16, st);
+  if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+  return status_of(launch_wy_export(buf, plan->chunk_tok0, plan->chunk_len, plan->n_chunk, H, K, V, (__bf16*)w,
+                                    (__bf16*)u, (__bf16*)kg, (__bf16*)Aqk, (__bf16*)qg, st));
+}
+
+int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* gk, const memt_gdn2_plan* plan,
+                    int64_t T, int H, int K, int V, const float* h0, float* snaps, float* ht, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
+  if (plan->n_chunk > 0 && (kg == nullptr || w == nullptr || u == nullptr || gk == nullptr ||
+                            plan->seq_chunk_offsets == nullptr))
+    return MEMT_GDN2_EINVAL;
+  if (snaps != nullptr && (plan->chunk_flags == nullptr || plan->chunk_block_ids == nullptr)) return MEMT_GDN2_EINVAL;
+  const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, false);
+  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
+    return MEMT_GDN2_EWORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const WyBuffers buf = wy_buffers(workspace, lay, false);
+  hipError_t e = launch_wy_import((const __bf16*)w, (const __bf16*)u, (const __bf16*)kg, gk, plan->chunk_tok0,
+                                  plan->chunk_len, plan->n_chunk, H, K, V, buf, st);
+  if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+  StateArgs sa{};
+  sa.in = buf;
+  sa.chunk_tok0 = plan->chunk_tok0;
+  sa.chunk_len = plan->chunk_len;
+  sa.seq_chunk_offsets = plan->seq_chunk_offsets;
+  sa.chunk_block_ids = plan->chunk_block_ids;
+  sa.chunk_flags = plan->chunk_flags;
+  sa.h0 = h0;
+  sa.ht = ht;
+  sa.snaps = snaps;
+  sa.o = nullptr;
+  sa.H = H;
+  sa.n_seq = plan->n_seq;
+  sa.scale = 1.f;
+  return status_of(launch_state(sa, K, V, false, st));
+}
+
+int memt_gdn2_read_fwd(const void* q, const float* snaps, void* o, const memt_gdn2_plan* plan, int64_t T, int H,
+                       int K, int V, float scale, void* stream) {
+  if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (plan->n_chunk > 0 && (q == nullptr || snaps == nullptr || o == nullptr || plan->chunk_block_ids == nullptr))
+    return MEMT_GDN2_EINVAL;
+  if (!aligned16(q) || !aligned16(snaps)) return MEMT_GDN2_EINVAL;
+  return status_of(launch_read_fwd((const __bf16*)q, snaps, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
+                                   plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, (hipStream_t)stream));
+}
+
+int memt_gdn2_rms_norm_gated(const void* x, const void* gate, const void* weight, void* out, int64_t rows, int dim,
+                             float eps, float softcap, int gate_kind, void* stream) {
+  if (rows < 0 || dim <= 0) return MEMT_GDN2_EINVAL;
+  if (rows > 0 && (x == nullptr || gate == nullptr || weight == nullptr || out == nullptr)) return MEMT_GDN2_EINVAL;
+  if (dim > 1024) return MEMT_GDN2_EUNSUPPORTED;
+  if (gate_kind != MEMT_GDN2_GATE_SOFTCAP_SILU && gate_kind != MEMT_GDN2_GATE_SIGMOID) return MEMT_GDN2_EINVAL;
+  if (gate_kind == MEMT_GDN2_GATE_SOFTCAP_SILU && !(softcap > 0.f)) return MEMT_GDN2_EINVAL;
+  return status_of(launch_rms_norm_gated((const __bf16*)x, (const __bf16*)gate, (const __bf16*)weight, (__bf16*)out,
+                                         rows, dim, eps, softcap, gate_kind, (hipStream_t)stream));
+}
+
+int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void* q, const void* gate,
+                            const void* weight, void* out, int B, int H, int K, int V, float scale, float eps,
+                            float softcap, int gate_kind, void* stream) {
+  if (B < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (B > 0 && (S == nullptr || q == nullptr || gate == nullptr || weight == nullptr || out == nullptr))
+    return MEMT_GDN2_EINVAL;
+  if (!aligned16(S)) return MEMT_GDN2_EINVAL;
+  if (gate_kind != MEMT_GDN2_GATE_SOFTCAP_SILU && gate_kind != MEMT_GDN2_GATE_SIGMOID) return MEMT_GDN2_EINVAL;
+  if (gate_kind == MEMT_GDN2_GATE_SOFTCAP_SILU && !(softcap > 0.f)) return MEMT_GDN2_EINVAL;
+  return status_of(launch_readout(S, slot_idx, (const __bf16*)q, (const __bf16*)gate, (const __bf16*)weight,
+                                  (__bf16*)out, B, H, K, V, scale, eps, softcap, gate_kind, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// Shared device helpers for the GDN-2 memory kernels (gfx950 / CDNA4, wave64).
+//
+// MFMA lane layouts used throughout (checked on gfx950 against a host matmul):
+//   v_mfma_f32_16x16x32_{bf16,f16}: A[16x32]: lane l holds A[l%16][8*(l/16) + 0..7]
+//                                    B[32x16]: lane l holds B[8*(l/16) + 0..7][l%16]
+//                                    C[16x16]: lane l holds C[4*(l/16) + 0..3][l%16]
+//   v_mfma_f32_16x16x4_f32:          A: lane l holds A[l%16][l/16]; B: B[l/16][l%16]; C as above.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace memt {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 1/ln(2) as the reference's cumsum scale (FLA/ops/utils/constant.py:10).
+constexpr float kRcpLn2 = 1.4426950216f;
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Native v_exp_f32 (base 2).  Inputs below -126 give denormal/zero results.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float bf16_to_f32(__bf16 x) { return (float)x; }
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round-to-nearest-even float -> bf16 (the conversion torch and Triton use).
+__device__ __forceinline__ __bf16 f32_to_bf16(float x) { return (__bf16)x; }
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+template <typename T>
+__device__ __forceinline__ float load_as_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_as_f32<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_as_f32<__bf16>(const __bf16* p) { return (float)*p; }
+
+// Wave64 sum reduction (all lanes receive the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace memt

@@ -1,0 +1,140 @@
+// Internal declarations of the GDN-2 kernels: workspace layout, fragment
+// orders and per-kernel argument blocks.  Not part of the C ABI.
+#pragma once
+
+#include "common.h"
+#include "../../include/memt_gdn2.h"
+
+namespace memt {
+
+constexpr int kChunk = 64;  // WY tile tokens (models/common/constants.py:3)
+
+// ---------------------------------------------------------------------------
+// Fragment orders.  The WY stage writes its outputs already arranged as the
+// MFMA operands the state scan loads, so every lane of the scan issues one
+// 16-byte (A operand) or 8-byte (C fragment) load and a wave reads a
+// contiguous 1 KiB / 512 B span.
+//
+//  A-frag of X[rows][red] (red % 32 == 0), 8 elements per lane:
+//     index = ((rt * red/32 + s) * 64 + lane) * 8 + e
+//     <-> X[16*rt + lane%16][32*s + 8*(lane/16) + e]
+//  C-frag of X[rows][n] (n % 16 == 0), 4 elements per lane:
+//     index = ((rt * n/16 + ct) * 64 + lane) * 4 + e
+//     <-> X[16*rt + 4*(lane/16) + e][16*ct + lane%16]
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ int afrag_index(int row, int col, int red) {
+  const int rt = row >> 4, s = col >> 5;
+  const int lane = (row & 15) + ((col >> 3) & 3) * 16;
+  return ((rt * (red >> 5) + s) * 64 + lane) * 8 + (col & 7);
+}
+__host__ __device__ __forceinline__ int cfrag_index(int row, int col, int n) {
+  const int rt = row >> 4, ct = col >> 4;
+  const int lane = (col & 15) + ((row >> 2) & 3) * 16;
+  return ((rt * (n >> 4) + ct) * 64 + lane) * 4 + (row & 3);
+}
+
+__host__ __device__ __forceinline__ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Per-(chunk, head) records of the WY stage, unit u = chunk * H + head.
+//   W     bf16 [64 x K]  A-frag (rows = tokens, red = K)       erase path
+//   kgT   f16  [K x 64]  A-frag of kg^T (rows = K, red = tokens) value path
+//   U     f16  [64 x V]  C-frag                                 value path
+//   decay f32  [K]       2^{gk_last}
+//   qg    bf16 [64 x K]  A-frag, q * 2^{gk}                     (causal output)
+//   Aqk   f16  [64 x 64] A-frag, scale * causal scores          (causal output)
+struct WyBuffers {
+  __bf16* W;
+  _Float16* kgT;
+  _Float16* U;
+  float* decay;
+  __bf16* qg;
+  _Float16* Aqk;
+};
+
+struct WyLayout {
+  size_t off_W, off_kg, off_U, off_decay, off_qg, off_Aqk, total;
+};
+
+inline WyLayout wy_layout(int n_chunk, int H, int K, int V, bool causal) {
+  const size_t units = (size_t)n_chunk * (size_t)H;
+  WyLayout l{};
+  size_t o = 0;
+  l.off_W = o;     o = align256(o + units * kChunk * K * 2);
+  l.off_kg = o;    o = align256(o + units * kChunk * K * 2);
+  l.off_U = o;     o = align256(o + units * kChunk * V * 2);
+  l.off_decay = o; o = align256(o + units * K * 4);
+  l.off_qg = o;    if (causal) o = align256(o + units * kChunk * K * 2);
+  l.off_Aqk = o;   if (causal) o = align256(o + units * kChunk * kChunk * 2);
+  l.total = o;
+  return l;
+}
+
+inline WyBuffers wy_buffers(void* ws, const WyLayout& l, bool causal) {
+  char* base = (char*)ws;
+  WyBuffers b;
+  b.W = (__bf16*)(base + l.off_W);
+  b.kgT = (_Float16*)(base + l.off_kg);
+  b.U = (_Float16*)(base + l.off_U);
+  b.decay = (float*)(base + l.off_decay);
+  b.qg = causal ? (__bf16*)(base + l.off_qg) : nullptr;
+  b.Aqk = causal ? (_Float16*)(base + l.off_Aqk) : nullptr;
+  return b;
+}
+
+struct WyArgs {
+  const __bf16* q;     // [T,H,K] (causal only)
+  const __bf16* k;     // [T,H,K]
+  const __bf16* v;     // [T,H,V]
+  const float* g;      // [T,H,K] natural-log decay, or log2 cumsum when g_cumulative
+  const void* beta;    // [T,H,V] f32 or bf16
+  const __bf16* b;     // [T,H,K] or null
+  const int32_t* chunk_tok0;
+  const int32_t* chunk_len;
+  int H;
+  float scale;
+  WyBuffers out;
+  __bf16* A_ref;       // optional [T,H,64] bf16 inverse (reference layout)
+};
+
+struct StateArgs {
+  WyBuffers in;
+  const int32_t* chunk_tok0;
+  const int32_t* chunk_len;
+  const int32_t* seq_chunk_offsets;
+  const int32_t* chunk_block_ids;
+  const int32_t* chunk_flags;
+  const float* h0;     // [N,H,K,V] or null
+  float* ht;           // [N,H,K,V] or null
+  float* snaps;        // [n_block,H,K,V] or null
+  __bf16* o;           // [T,H,V] (causal) or null
+  int H;
+  int n_seq;
+  float scale;
+};
+
+// Launchers (return hipError_t of the launch).
+hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bool g_cumulative,
+                     bool beta_bf16, hipStream_t stream);
+hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream_t stream);
+hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
+                           const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
+                           int K, int V, float scale, hipStream_t stream);
+hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
+                          const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
+                          float eps, float softcap, int gate_kind, hipStream_t stream);
+hipError_t launch_rms_norm_gated(const __bf16* x, const __bf16* gate, const __bf16* weight, __bf16* out,
+                                 int64_t rows, int dim, float eps, float softcap, int gate_kind,
+                                 hipStream_t stream);
+hipError_t launch_l2norm(const void* x, bool x_bf16, void* y, bool y_bf16, float* rstd, int64_t rows,
+                         int dim, float eps, hipStream_t stream);
+hipError_t launch_cumsum(const void* g, bool g_bf16, float* gk, const int32_t* chunk_tok0,
+                         const int32_t* chunk_len, int n_chunk, int H, int S, float scale, bool reverse,
+                         hipStream_t stream);
+hipError_t launch_wy_export(const WyBuffers& in, const int32_t* chunk_tok0, const int32_t* chunk_len,
+                            int n_chunk, int H, int K, int V, __bf16* w, __bf16* u, __bf16* kg,
+                            __bf16* Aqk, __bf16* qg, hipStream_t stream);
+hipError_t launch_wy_import(const __bf16* w, const __bf16* u, const __bf16* kg, const float* gk,
+                            const int32_t* chunk_tok0, const int32_t* chunk_len, int n_chunk, int H,
+                            int K, int V, WyBuffers out, hipStream_t stream);
+
+}  // namespace memt

@@ -1,0 +1,386 @@
+// Readout, normalisation and layout kernels of the GDN-2 memory path.
+#include "gdn2_internal.h"
+
+namespace memt {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Snapshot reader (models/qwen/ops/_triton/read.py:22-71): per (chunk, head),
+// o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32 accumulation.
+// Wave w handles token rows [16w, 16w + 16) and all V columns.
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict__ q,
+                                                       const float* __restrict__ snaps,
+                                                       __bf16* __restrict__ o, const int32_t* chunk_tok0,
+                                                       const int32_t* chunk_len, const int32_t* block_ids,
+                                                       int H, float scale) {
+  constexpr int SKP = K + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 S_lds[V * SKP];  // column-major bf16(S)
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
+  const float* Sp = snaps + ((size_t)block_ids[chunk] * H + h) * K * V;
+  for (int idx = tid; idx < K * V / 4; idx += 256) {
+    const int row = idx / (V / 4), c4 = (idx % (V / 4)) * 4;
+    const f32x4 s4 = *(const f32x4*)(Sp + (size_t)row * V + c4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) S_lds[(c4 + e) * SKP + row] = (__bf16)s4[e];
+  }
+  __syncthreads();
+  const int t = 16 * w + lr;
+  f32x4 acc[V / 16];
+#pragma unroll
+  for (int ct = 0; ct < V / 16; ++ct) acc[ct] = zero4();
+#pragma unroll
+  for (int s = 0; s < K / 32; ++s) {
+    bf16x8 qa;
+    if (t < len) {
+      qa = *(const bf16x8*)(q + ((size_t)(tok0 + t) * H + h) * K + 32 * s + 8 * lg);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qa[e] = (__bf16)0.f;
+    }
+#pragma unroll
+    for (int ct = 0; ct < V / 16; ++ct) {
+      const bf16x8 sb = *(const bf16x8*)(&S_lds[(16 * ct + lr) * SKP + 32 * s + 8 * lg]);
+      acc[ct] = mfma_bf16(qa, sb, acc[ct]);
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < V / 16; ++ct)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int tt = 16 * w + 4 * lg + e;
+      if (tt < len) o[((size_t)(tok0 + tt) * H + h) * V + 16 * ct + lr] = (__bf16)(acc[ct][e] * scale);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The epilogue of MemTRMSNormGated (models/qwen/layer.py:22-31) applied to one
+// value of a row whose mean square is `ms`:
+//   y = bf16(x * rsqrt(ms + eps)); y = bf16(w * y); out = bf16(y * gate_fn(g)).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gate_value(float g, float softcap, int gate_kind) {
+  if (gate_kind == MEMT_GDN2_GATE_SIGMOID) return 1.f / (1.f + expf(-g));
+  const float silu = g / (1.f + expf(-g));
+  return softcap * tanhf(silu / softcap);
+}
+
+__device__ __forceinline__ __bf16 norm_gate_one(float x, float rs, float wt, float g, float softcap,
+                                                int gate_kind) {
+  const float y = (float)(__bf16)(x * rs);
+  const float yw = (float)(__bf16)(wt * y);
+  return (__bf16)(yw * gate_value(g, softcap, gate_kind));
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode readout: one workgroup per (sequence, head).
+//   r = bf16(scale * q . S) (fp32 S, fp32 accumulation), then the epilogue.
+// Thread (rg, cg) streams rows [rg*RPT, (rg+1)*RPT) of columns [4cg, 4cg+4)
+// with 16-byte loads; a wave covers contiguous rows of the fp32 state.
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ S, const int32_t* slot_idx,
+                                                      const __bf16* __restrict__ q,
+                                                      const __bf16* __restrict__ gate,
+                                                      const __bf16* __restrict__ weight,
+                                                      __bf16* __restrict__ out, int H, float scale,
+                                                      float eps, float softcap, int gate_kind) {
+  constexpr int CG = V / 4;          // float4 column groups
+  constexpr int RG = 256 / CG;       // row groups
+  constexpr int RPT = K / RG;        // rows per thread
+  static_assert(RG * CG == 256 && RPT * RG == K, "readout tiling");
+  __shared__ float q_s[K];
+  __shared__ float part[RG][V];
+  __shared__ float red[4];
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x;
+  const int slot = slot_idx ? slot_idx[b] : b;
+  const float* Sp = S + ((size_t)slot * H + h) * K * V;
+  const size_t row = (size_t)b * H + h;
+  if (tid < K) q_s[tid] = (float)q[row * K + tid];
+  __syncthreads();
+  const int cg = tid % CG, rg = tid / CG;
+  f32x4 acc = zero4();
+#pragma unroll 8
+  for (int i = 0; i < RPT; ++i) {
+    const int k = rg * RPT + i;
+    const f32x4 s4 = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)k * V + 4 * cg));
+    const float qk = q_s[k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = fmaf(qk, s4[e], acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) part[rg][4 * cg + e] = acc[e];
+  __syncthreads();
+  float r = 0.f, sq = 0.f;
+  if (tid < V) {
+    float sum = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < RG; ++g2) sum += part[g2][tid];
+    r = (float)(__bf16)(sum * scale);  // the reader's bf16 output
+    sq = r * r;
+  }
+  sq = wave_sum(sq);
+  if ((tid & 63) == 0) red[tid >> 6] = sq;
+  __syncthreads();
+  if (tid < V) {
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < (V + 63) / 64; ++i) tot += red[i];
+    const float rs = rsqrtf(tot / (float)V + eps);
+    const float g = (float)gate[row * V + tid];
+    out[row * V + tid] = norm_gate_one(r, rs, (float)weight[tid], g, softcap, gate_kind);
+  }
+}
+
+// MemTRMSNormGated over rows of `dim` (one wave per row, dim <= 1024).
+__global__ __launch_bounds__(256) void rms_norm_gated_kernel(const __bf16* __restrict__ x,
+                                                             const __bf16* __restrict__ gate,
+                                                             const __bf16* __restrict__ weight,
+                                                             __bf16* __restrict__ out, int64_t rows,
+                                                             int dim, float eps, float softcap,
+                                                             int gate_kind) {
+  const int64_t rrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (rrow >= rows) return;
+  const __bf16* xr = x + rrow * dim;
+  float vals[16];
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = lane + 64 * i;
+    vals[i] = (c < dim) ? (float)xr[c] : 0.f;
+    sq += vals[i] * vals[i];
+  }
+  sq = wave_sum(sq);
+  const float rs = rsqrtf(sq / (float)dim + eps);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = lane + 64 * i;
+    if (c < dim)
+      out[rrow * dim + c] =
+          norm_gate_one(vals[i], rs, (float)weight[c], (float)gate[rrow * dim + c], softcap, gate_kind);
+  }
+}
+
+// FLA l2norm_fwd (FLA/modules/l2norm.py:95-109): one wave per row, dim <= 512.
+template <bool XBF, bool YBF>
+__global__ __launch_bounds__(256) void l2norm_kernel(const void* __restrict__ x, void* __restrict__ y,
+                                                     float* __restrict__ rstd, int64_t rows, int dim,
+                                                     float eps) {
+  const int64_t rrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (rrow >= rows) return;
+  float vals[8];
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane + 64 * i;
+    float v = 0.f;
+    if (c < dim) v = XBF ? (float)((const __bf16*)x)[rrow * dim + c] : ((const float*)x)[rrow * dim + c];
+    vals[i] = v;
+    sq += v * v;
+  }
+  sq = wave_sum(sq);
+  const float rs = 1.f / sqrtf(sq + eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = lane + 64 * i;
+    if (c < dim) {
+      const float v = vals[i] * rs;
+      if (YBF)
+        ((__bf16*)y)[rrow * dim + c] = (__bf16)v;
+      else
+        ((float*)y)[rrow * dim + c] = v;
+    }
+  }
+  if (rstd != nullptr && lane == 0) rstd[rrow] = rs;
+}
+
+// Chunk-local cumsum (FLA/ops/utils/cumsum.py:116-133): one thread per
+// (chunk, head, channel), sequential over the chunk's tokens.
+template <bool GBF>
+__global__ __launch_bounds__(256) void cumsum_kernel(const void* __restrict__ g, float* __restrict__ gk,
+                                                     const int32_t* chunk_tok0, const int32_t* chunk_len,
+                                                     int H, int S, float scale, int reverse) {
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const int c = blockIdx.z * 256 + threadIdx.x;
+  if (c >= S) return;
+  const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
+  float run = 0.f;
+  for (int i = 0; i < len; ++i) {
+    const int t = reverse ? (len - 1 - i) : i;
+    const size_t off = ((size_t)(tok0 + t) * H + h) * S + c;
+    run += GBF ? (float)((const __bf16*)g)[off] : ((const float*)g)[off];
+    gk[off] = run * scale;
+  }
+}
+
+// Workspace fragments -> the reference's [T, H, D] bf16 layouts.
+template <int K, int V>
+__global__ __launch_bounds__(256) void wy_export_kernel(WyBuffers in, const int32_t* chunk_tok0,
+                                                        const int32_t* chunk_len, int H, __bf16* w,
+                                                        __bf16* u, __bf16* kg, __bf16* Aqk, __bf16* qg) {
+  constexpr int C = kChunk;
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const size_t unit = (size_t)chunk * H + h;
+  const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
+  for (int idx = threadIdx.x; idx < len * K; idx += 256) {
+    const int t = idx / K, c = idx % K;
+    const size_t dst = ((size_t)(tok0 + t) * H + h) * K + c;
+    if (w) w[dst] = in.W[unit * C * K + afrag_index(t, c, K)];
+    if (kg) kg[dst] = (__bf16)(float)in.kgT[unit * C * K + afrag_index(c, t, C)];
+    if (qg && in.qg) qg[dst] = in.qg[unit * C * K + afrag_index(t, c, K)];
+  }
+  for (int idx = threadIdx.x; idx < len * V; idx += 256) {
+    const int t = idx / V, c = idx % V;
+    if (u) u[((size_t)(tok0 + t) * H + h) * V + c] = (__bf16)(float)in.U[unit * C * V + cfrag_index(t, c, V)];
+  }
+  if (Aqk && in.Aqk) {
+    for (int idx = threadIdx.x; idx < len * C; idx += 256) {
+      const int t = idx / C, j = idx % C;
+      Aqk[((size_t)(tok0 + t) * H + h) * C + j] = (__bf16)(float)in.Aqk[unit * C * C + afrag_index(t, j, C)];
+    }
+  }
+}
+
+// The reference's [T, H, D] WY tensors -> workspace fragments (rows past the
+// chunk end are zero), decay = 2^{gk at the chunk's last token}.
+template <int K, int V>
+__global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const __bf16* u, const __bf16* kg,
+                                                        const float* gk, const int32_t* chunk_tok0,
+                                                        const int32_t* chunk_len, int H, WyBuffers out) {
+  constexpr int C = kChunk;
+  const int chunk = blockIdx.x, h = blockIdx.y;
+  const size_t unit = (size_t)chunk * H + h;
+  const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
+  for (int idx = threadIdx.x; idx < C * K; idx += 256) {
+    const int t = idx / K, c = idx % K;
+    const size_t src = ((size_t)(tok0 + t) * H + h) * K + c;
+    const bool ok = t < len;
+    out.W[unit * C * K + afrag_index(t, c, K)] = ok ? w[src] : (__bf16)0.f;
+    out.kgT[unit * C * K + afrag_index(c, t, C)] = (_Float16)(ok ? (float)kg[src] : 0.f);
+  }
+  for (int idx = threadIdx.x; idx < C * V; idx += 256) {
+    const int t = idx / V, c = idx % V;
+    const bool ok = t < len;
+    out.U[unit * C * V + cfrag_index(t, c, V)] =
+        (_Float16)(ok ? (float)u[((size_t)(tok0 + t) * H + h) * V + c] : 0.f);
+  }
+  for (int c = threadIdx.x; c < K; c += 256)
+    out.decay[unit * K + c] = fast_exp2(gk[((size_t)(tok0 + len - 1) * H + h) * K + c]);
+}
+
+}  // namespace
+
+hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
+                           const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
+                           int K, int V, float scale, hipStream_t stream) {
+  if (n_chunk == 0) return hipSuccess;
+  dim3 grid(n_chunk, H), block(256);
+  if (K == 64 && V == 64)
+    hipLaunchKernelGGL((read_fwd_kernel<64, 64>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
+                       chunk_block_ids, H, scale);
+  else if (K == 128 && V == 128)
+    hipLaunchKernelGGL((read_fwd_kernel<128, 128>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
+                       chunk_block_ids, H, scale);
+  else if (K == 256 && V == 256)
+    hipLaunchKernelGGL((read_fwd_kernel<256, 256>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
+                       chunk_block_ids, H, scale);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
+                          const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
+                          float eps, float softcap, int gate_kind, hipStream_t stream) {
+  if (B == 0) return hipSuccess;
+  dim3 grid(B * H), block(256);
+#define MEMT_RO(KK, VV)                                                                                   \
+  if (K == KK && V == VV) {                                                                               \
+    hipLaunchKernelGGL((readout_kernel<KK, VV>), grid, block, 0, stream, S, slot_idx, q, gate, weight, out, \
+                       H, scale, eps, softcap, gate_kind);                                                \
+    return hipGetLastError();                                                                             \
+  }
+  MEMT_RO(64, 64)
+  MEMT_RO(128, 128)
+  MEMT_RO(256, 256)
+#undef MEMT_RO
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_rms_norm_gated(const __bf16* x, const __bf16* gate, const __bf16* weight, __bf16* out,
+                                 int64_t rows, int dim, float eps, float softcap, int gate_kind,
+                                 hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  hipLaunchKernelGGL(rms_norm_gated_kernel, grid, block, 0, stream, x, gate, weight, out, rows, dim, eps, softcap,
+                     gate_kind);
+  return hipGetLastError();
+}
+
+hipError_t launch_l2norm(const void* x, bool x_bf16, void* y, bool y_bf16, float* rstd, int64_t rows, int dim,
+                         float eps, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  if (x_bf16 && y_bf16)
+    hipLaunchKernelGGL((l2norm_kernel<true, true>), grid, block, 0, stream, x, y, rstd, rows, dim, eps);
+  else if (x_bf16 && !y_bf16)
+    hipLaunchKernelGGL((l2norm_kernel<true, false>), grid, block, 0, stream, x, y, rstd, rows, dim, eps);
+  else if (!x_bf16 && y_bf16)
+    hipLaunchKernelGGL((l2norm_kernel<false, true>), grid, block, 0, stream, x, y, rstd, rows, dim, eps);
+  else
+    hipLaunchKernelGGL((l2norm_kernel<false, false>), grid, block, 0, stream, x, y, rstd, rows, dim, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_cumsum(const void* g, bool g_bf16, float* gk, const int32_t* chunk_tok0,
+                         const int32_t* chunk_len, int n_chunk, int H, int S, float scale, bool reverse,
+                         hipStream_t stream) {
+  if (n_chunk == 0) return hipSuccess;
+  dim3 grid(n_chunk, H, (S + 255) / 256), block(256);
+  if (g_bf16)
+    hipLaunchKernelGGL((cumsum_kernel<true>), grid, block, 0, stream, g, gk, chunk_tok0, chunk_len, H, S, scale,
+                       reverse ? 1 : 0);
+  else
+    hipLaunchKernelGGL((cumsum_kernel<false>), grid, block, 0, stream, g, gk, chunk_tok0, chunk_len, H, S, scale,
+                       reverse ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_wy_export(const WyBuffers& in, const int32_t* chunk_tok0, const int32_t* chunk_len, int n_chunk,
+                            int H, int K, int V, __bf16* w, __bf16* u, __bf16* kg, __bf16* Aqk, __bf16* qg,
+                            hipStream_t stream) {
+  if (n_chunk == 0) return hipSuccess;
+  dim3 grid(n_chunk, H), block(256);
+  if (K == 64 && V == 64)
+    hipLaunchKernelGGL((wy_export_kernel<64, 64>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
+                       Aqk, qg);
+  else if (K == 128 && V == 128)
+    hipLaunchKernelGGL((wy_export_kernel<128, 128>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
+                       Aqk, qg);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_wy_import(const __bf16* w, const __bf16* u, const __bf16* kg, const float* gk,
+                            const int32_t* chunk_tok0, const int32_t* chunk_len, int n_chunk, int H, int K, int V,
+                            WyBuffers out, hipStream_t stream) {
+  if (n_chunk == 0) return hipSuccess;
+  dim3 grid(n_chunk, H), block(256);
+  if (K == 64 && V == 64)
+    hipLaunchKernelGGL((wy_import_kernel<64, 64>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
+                       out);
+  else if (K == 128 && V == 128)
+    hipLaunchKernelGGL((wy_import_kernel<128, 128>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
+                       out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace memt

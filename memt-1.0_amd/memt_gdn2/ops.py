@@ -1,0 +1,401 @@
+"""GDN-2 native-memory operators on the HIP library.
+
+Each function keeps the name, arguments, layouts and error behaviour of the
+reference operator it replaces (cited per function), so the SGLang plugin can
+swap imports.  Outputs are allocated with torch on the inputs' device
+(caching allocator); kernels run on torch's current stream.  There is no CPU
+or PyTorch fallback: a missing library or a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .layout import WY_TILE_TOKENS, ChunkPlan, build_chunk_plan, packed_plan, plan_from_cu_seqlens
+
+__all__ = [
+    "l2norm_fwd",
+    "l2norm",
+    "chunk_local_cumsum",
+    "chunk_gdn2_fwd_intra",
+    "memt_gdn2_fwd_h",
+    "memt_gdn2_read_fwd",
+    "snapshot_read",
+    "token_memory_packed",
+    "token_memory_packed_flash",
+    "chunk_gdn2",
+    "rms_norm_gated",
+    "readout_fused",
+    "workspace_bytes",
+]
+
+_DT = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
+_GATES = {"softcap_silu": _lib.GATE_SOFTCAP_SILU, "silu": _lib.GATE_SOFTCAP_SILU, "sigmoid": _lib.GATE_SIGMOID}
+_OUT = {"none": _lib.OUT_NONE, "snapshot": _lib.OUT_SNAPSHOT, "causal": _lib.OUT_CAUSAL}
+
+
+def _contig(*ts):
+    return [None if t is None else t.contiguous() for t in ts]
+
+
+def workspace_bytes(num_chunk: int, H: int, K: int, V: int, out_mode: str = "snapshot") -> int:
+    """Device workspace of one chunked update (fragments of W, kg, U, ...)."""
+    return int(_lib.load().memt_gdn2_chunk_update_workspace_size(num_chunk, H, K, V, _OUT[out_mode]))
+
+
+def _workspace(device, nbytes: int) -> torch.Tensor:
+    # torch's caching allocator hands out 512-byte aligned blocks.
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+    if ws.data_ptr() % 256:
+        raise RuntimeError("workspace is not 256-byte aligned")
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# FLA helpers
+# ---------------------------------------------------------------------------
+
+
+def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6, output_dtype: torch.dtype | None = None):
+    """``y = x / sqrt(sum(x^2) + eps)`` per row; returns ``(y, rstd)``
+    (FLA/modules/l2norm.py:147-197, D <= 512)."""
+    lib = _lib.load()
+    _lib.require_gpu(x)
+    shape = x.shape
+    x2 = x.contiguous().view(-1, shape[-1])
+    out_dtype = x.dtype if output_dtype is None else output_dtype
+    if x2.dtype not in _DT or out_dtype not in _DT:
+        raise ValueError("l2norm_fwd supports bf16 and fp32")
+    y = torch.empty(x2.shape, dtype=out_dtype, device=x.device)
+    rstd = torch.empty(x2.shape[0], dtype=torch.float32, device=x.device)
+    if shape[-1] > 512:
+        raise RuntimeError("This layer doesn't support feature dim >= 512 on this path.")
+    _lib.check(
+        lib.memt_gdn2_l2norm_fwd(x2.data_ptr(), _DT[x2.dtype], y.data_ptr(), _DT[out_dtype], rstd.data_ptr(),
+                                 x2.shape[0], shape[-1], float(eps), _lib.stream_of(x.device)),
+        "l2norm_fwd",
+    )
+    return y.view(shape), rstd.view(shape[:-1])
+
+
+def l2norm(inputs: torch.Tensor) -> torch.Tensor:
+    """models/qwen/ops/normalization.py:6-8."""
+    return l2norm_fwd(inputs)[0]
+
+
+def _dense_or_varlen_plan(B: int, T: int, device, cu_seqlens, chunk_size: int) -> ChunkPlan:
+    if cu_seqlens is not None:
+        if B != 1:
+            raise ValueError("Only batch size 1 is supported when cu_seqlens are provided")
+        return plan_from_cu_seqlens(cu_seqlens, T, device, wy_tile_tokens=chunk_size)
+    cu = [b * T for b in range(B + 1)]
+    return build_chunk_plan(cu, cu, chunk_size, device=device)
+
+
+def chunk_local_cumsum(g: torch.Tensor, chunk_size: int, reverse: bool = False, scale: float | None = None,
+                       cu_seqlens=None, head_first: bool = False, output_dtype: torch.dtype | None = torch.float,
+                       chunk_indices=None, **kwargs) -> torch.Tensor:
+    """Chunk-local prefix sum of ``g`` [B,T,H,S] (or [B,T,H]) along T
+    (FLA/ops/utils/cumsum.py:444-486).  ``chunk_indices`` is accepted for
+    signature parity; chunks are derived from ``cu_seqlens`` and ``chunk_size``."""
+    lib = _lib.load()
+    _lib.require_gpu(g)
+    if head_first:
+        raise ValueError("head_first layouts are not used by the memory path")
+    if output_dtype not in (None, torch.float):
+        raise ValueError("chunk_local_cumsum writes fp32")
+    if chunk_size != 2 ** (chunk_size.bit_length() - 1) or chunk_size > 64:
+        raise ValueError("chunk_size must be a power of 2 <= 64")
+    if g.ndim == 3:
+        g4 = g.unsqueeze(-1)
+    elif g.ndim == 4:
+        g4 = g
+    else:
+        raise ValueError(f"Unsupported input shape {g.shape}, which should be (B, T, H, D) or (B, T, H)")
+    g4 = g4.contiguous()
+    if g4.dtype not in _DT:
+        raise ValueError("chunk_local_cumsum supports bf16 and fp32 inputs")
+    B, T, H, S = g4.shape
+    plan = _dense_or_varlen_plan(B, T, g.device, cu_seqlens, chunk_size)
+    out = torch.empty(g4.shape, dtype=torch.float32, device=g.device)
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_chunk_local_cumsum(g4.data_ptr(), _DT[g4.dtype], out.data_ptr(), ctypes.byref(p), H, S,
+                                         1.0 if scale is None else float(scale), int(bool(reverse)),
+                                         _lib.stream_of(g.device)),
+        "chunk_local_cumsum",
+    )
+    return out.view(g.shape)
+
+
+# ---------------------------------------------------------------------------
+# WY stage, state scan and snapshot reader
+# ---------------------------------------------------------------------------
+
+
+def _check_tokens(name, t, T, H, D):
+    if t.ndim != 4 or t.shape[0] != 1 or t.shape[1] != T or t.shape[2] != H or t.shape[3] != D:
+        raise ValueError(f"{name} must be [1, {T}, {H}, {D}], got {tuple(t.shape)}")
+
+
+def chunk_gdn2_fwd_intra(q, k, v, gk, b, w_gate, scale, cu_seqlens=None, chunk_size: int = 64, chunk_indices=None,
+                         safe_gate: bool = False, disable_recompute: bool = False):
+    """WY auxiliaries of every chunk (FLA/ops/gdn2/chunk_intra.py:693-787).
+
+    Returns ``(w, u, qg, kg, Aqk, Akk)`` in the reference layouts (bf16
+    [B,T,H,*]); ``qg`` is None unless ``disable_recompute``.  ``gk`` is the
+    chunk-local cumulative decay in log2 units; ``b`` may be None (unit erase).
+    """
+    lib = _lib.load()
+    _lib.require_gpu(q, k, v, gk, b, w_gate)
+    if safe_gate:
+        raise ValueError("safe_gate=True is not used by the memory path")
+    if chunk_size != WY_TILE_TOKENS:
+        raise ValueError("chunk_size must be 64")
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    if B != 1 and cu_seqlens is not None:
+        raise ValueError("Only batch size 1 is supported when cu_seqlens are provided")
+    q, k, v, gk, b, w_gate = _contig(q, k, v, gk, b, w_gate)
+    plan = _dense_or_varlen_plan(B, T, k.device, cu_seqlens, chunk_size)
+    dev = k.device
+    w = torch.empty_like(k)
+    u = torch.empty_like(v)
+    kg = torch.empty_like(k)
+    Aqk = torch.zeros(B, T, H, chunk_size, dtype=k.dtype, device=dev)
+    Akk = torch.zeros(B, T, H, chunk_size, dtype=k.dtype, device=dev)
+    qg = torch.empty_like(q) if disable_recompute else None
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "causal"))
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_wy_fwd(
+            _lib.ptr(q), k.data_ptr(), v.data_ptr(), gk.data_ptr(), _lib.ptr(b), w_gate.data_ptr(), _DT[w_gate.dtype],
+            ctypes.byref(p), B * T, H, K, V, float(scale), w.data_ptr(), u.data_ptr(), kg.data_ptr(),
+            Akk.data_ptr(), Aqk.data_ptr(), _lib.ptr(qg), ws.data_ptr(), ws.numel(), _lib.stream_of(dev)),
+        "chunk_gdn2_fwd_intra",
+    )
+    return w, u, qg, kg, Aqk, Akk
+
+
+def memt_gdn2_fwd_h(kg, w_wy, u_wy, gk, plan: ChunkPlan, initial_state=None, output_final_state: bool = True):
+    """Scan WY tiles into fp32 snapshots and final states
+    (models/qwen/ops/_triton/state.py:127-174).  Returns ``(snaps, final)``."""
+    lib = _lib.load()
+    _lib.require_gpu(kg, w_wy, u_wy, gk, initial_state)
+    _, T, H, K = kg.shape
+    V = u_wy.shape[-1]
+    kg, w_wy, u_wy, gk, initial_state = _contig(kg, w_wy, u_wy, gk, initial_state)
+    dev = kg.device
+    snaps = torch.zeros(plan.num_block, H, K, V, dtype=torch.float32, device=dev)
+    final = torch.zeros(plan.num_sample, H, K, V, dtype=torch.float32, device=dev) if output_final_state else None
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "none"))
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_fwd_h(kg.data_ptr(), w_wy.data_ptr(), u_wy.data_ptr(), gk.data_ptr(), ctypes.byref(p), T, H, K,
+                            V, _lib.ptr(initial_state), snaps.data_ptr(), _lib.ptr(final), ws.data_ptr(), ws.numel(),
+                            _lib.stream_of(dev)),
+        "memt_gdn2_fwd_h",
+    )
+    return snaps, final
+
+
+def memt_gdn2_read_fwd(q: torch.Tensor, snaps: torch.Tensor, plan: ChunkPlan, scale: float,
+                       out_dtype: torch.dtype) -> torch.Tensor:
+    """Every token reads its block's snapshot: ``bf16(scale * q . bf16(S))``
+    (models/qwen/ops/read.py:10-39)."""
+    lib = _lib.load()
+    _lib.require_gpu(q, snaps)
+    if out_dtype != torch.bfloat16:
+        raise ValueError("memt_gdn2_read_fwd writes bf16")
+    _, L, H, K = q.shape
+    V = snaps.shape[-1]
+    q, snaps = _contig(q, snaps)
+    out = torch.empty(1, L, H, V, device=q.device, dtype=out_dtype)
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_read_fwd(q.data_ptr(), snaps.data_ptr(), out.data_ptr(), ctypes.byref(p), L, H, K, V,
+                               float(scale), _lib.stream_of(q.device)),
+        "memt_gdn2_read_fwd",
+    )
+    return out
+
+
+def snapshot_read(query, states, lengths, scale, *, bf16_accumulator_output: bool = False):
+    """Flash reader (models/deepseek/ops/read.py:6-31): each sample's tokens
+    read ``scale * q . bf16(S_sample)`` with fp32 accumulation, bf16 out."""
+    samples = [0]
+    for n in lengths:
+        samples.append(samples[-1] + int(n))
+    plan = build_chunk_plan(samples, samples, device=query.device)
+    return memt_gdn2_read_fwd(query, states, plan, scale, out_dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# The packed commit (plugin drop-in) and the generic chunked update
+# ---------------------------------------------------------------------------
+
+
+def _chunk_update(q, k, v, g, beta, b, h0, read_states, plan: ChunkPlan, scale: float, out_mode: str,
+                  want_final: bool = True, snaps=None):
+    lib = _lib.load()
+    _lib.require_gpu(q, k, v, g, beta, b, h0, read_states)
+    _, T, H, K = k.shape
+    V = v.shape[-1]
+    if plan.total_tokens != T:
+        raise ValueError("plan does not cover the token axis")
+    for name, t, D in (("k", k, K), ("v", v, V), ("log_decay", g, K), ("write", beta, V)):
+        _check_tokens(name, t, T, H, D)
+    if q is not None:
+        _check_tokens("q", q, T, H, K)
+    if b is not None:
+        _check_tokens("erase", b, T, H, K)
+    for name, t, dt in (("q", q, torch.bfloat16), ("k", k, torch.bfloat16), ("v", v, torch.bfloat16),
+                        ("log_decay", g, torch.float32), ("erase", b, torch.bfloat16)):
+        if t is not None and t.dtype != dt:
+            raise ValueError(f"{name} must be {dt}, got {t.dtype}")
+    if beta.dtype not in _DT:
+        raise ValueError("write gate must be bf16 or fp32")
+    expected = (plan.num_sample, H, K, V)
+    for name, t in (("write_states", h0), ("read_states", read_states)):
+        if t is not None and (tuple(t.shape) != expected or t.dtype != torch.float32):
+            raise ValueError(f"{name} must be fp32 {expected}")
+    q, k, v, g, beta, b, h0, read_states = _contig(q, k, v, g, beta, b, h0, read_states)
+    dev = k.device
+    final = torch.empty(plan.num_sample, H, K, V, dtype=torch.float32, device=dev) if want_final else None
+    o = torch.empty(1, T, H, V, dtype=torch.bfloat16, device=dev) if out_mode != "none" else None
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, out_mode))
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_chunk_update(
+            _lib.ptr(q), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), _DT[beta.dtype], _lib.ptr(b),
+            _lib.ptr(h0), _lib.ptr(final), _lib.ptr(read_states), _lib.ptr(snaps), _lib.ptr(o), ctypes.byref(p), T,
+            H, K, V, float(scale), _OUT[out_mode], ws.data_ptr(), ws.numel(), _lib.stream_of(dev)),
+        "chunk_update",
+    )
+    return o, final
+
+
+def token_memory_packed(q, k, v, log_decay, write, read_states, write_states, *, erase, lengths, scale,
+                        chunk_tokens):
+    """Commit packed samples and read each sample's incoming snapshot
+    (models/qwen/ops/packed.py:34-81).
+
+    Every sample ``n`` scans its tokens from ``write_states[n]`` (result:
+    ``final[n]``) while all its tokens read ``read_states[n]``.  ``erase`` is
+    the channel erase gate [1,T,H,K] bf16, or None for the unit gate the
+    stable variant passes (models/qwen/layer.py:97).  Returns
+    ``(read [1,T,H,V] bf16, final [N,H,K,V] fp32)``.
+    """
+    if not lengths or any(int(n) <= 0 for n in lengths):
+        raise ValueError("Packed sample lengths must be positive")
+    plan = packed_plan(lengths, k.device, chunk_tokens=chunk_tokens)
+    return _chunk_update(q, k, v, log_decay, write, erase, write_states, read_states, plan, scale, "snapshot")
+
+
+def token_memory_packed_flash(q, k, v, log_decay, write, read_states, write_states, *, lengths, scale,
+                              chunk_tokens):
+    """Flash variant (models/deepseek/ops/packed.py:70-108): unit erase gate,
+    every sample reads its incoming state."""
+    return token_memory_packed(q, k, v, log_decay, write, read_states, write_states, erase=None, lengths=lengths,
+                               scale=scale, chunk_tokens=chunk_tokens)
+
+
+def chunk_gdn2(q, k, v, g, beta, *, b=None, initial_state=None, output_final_state: bool = True, cu_seqlens=None,
+               scale: float | None = None, out_mode: str = "causal", chunk_tokens=None):
+    """Chunked GDN-2 over independent sequences (packed by ``cu_seqlens``).
+
+    ``out_mode="causal"``: ``o_t = scale * q_t^T S_t``; ``"snapshot"``: every
+    token reads its sequence's initial state (MemT's commit read);
+    ``"none"``: state only.  Returns ``(o, ht)``.
+    """
+    if out_mode not in _OUT:
+        raise ValueError(f"out_mode must be one of {sorted(_OUT)}")
+    B, T, H, K = k.shape
+    if B != 1:
+        if cu_seqlens is not None:
+            raise ValueError("Only batch size 1 is supported when cu_seqlens are provided")
+        cu = [i * T for i in range(B + 1)]
+        flat = lambda t: None if t is None else t.reshape(1, B * T, *t.shape[2:])  # noqa: E731
+        o, ht = chunk_gdn2(flat(q), flat(k), flat(v), flat(g), flat(beta), b=flat(b), initial_state=initial_state,
+                           output_final_state=output_final_state, cu_seqlens=cu, scale=scale, out_mode=out_mode,
+                           chunk_tokens=chunk_tokens)
+        return (None if o is None else o.view(B, T, H, -1)), ht
+    plan = plan_from_cu_seqlens(cu_seqlens, T, k.device, chunk_tokens=chunk_tokens)
+    if scale is None:
+        scale = K ** -0.5
+    read_states = initial_state
+    if out_mode == "snapshot" and initial_state is None:
+        read_states = torch.zeros(plan.num_sample, H, K, v.shape[-1], dtype=torch.float32, device=k.device)
+    return _chunk_update(q if out_mode != "none" else None, k, v, g, beta, b, initial_state,
+                         read_states if out_mode == "snapshot" else None, plan, scale, out_mode,
+                         want_final=output_final_state)
+
+
+# ---------------------------------------------------------------------------
+# Readout epilogue
+# ---------------------------------------------------------------------------
+
+
+def rms_norm_gated(x, gate, weight, *, eps: float, softcap: float = 2.0, gate_kind: str = "softcap_silu"):
+    """``MemTRMSNormGated.forward`` (models/qwen/layer.py:22-31) over the last axis."""
+    lib = _lib.load()
+    _lib.require_gpu(x, gate, weight)
+    if gate_kind not in _GATES:
+        raise ValueError(f"gate_kind must be one of {sorted(_GATES)}")
+    if x.shape != gate.shape or weight.shape != (x.shape[-1],):
+        raise ValueError("x/gate must match and weight must be [dim]")
+    if x.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("rms_norm_gated expects bf16 x, gate and weight")
+    x2, g2, w2 = _contig(x, gate, weight)
+    out = torch.empty_like(x2)
+    dim = x.shape[-1]
+    _lib.check(
+        lib.memt_gdn2_rms_norm_gated(x2.data_ptr(), g2.data_ptr(), w2.data_ptr(), out.data_ptr(), x2.numel() // dim,
+                                     dim, float(eps), float(softcap), _GATES[gate_kind], _lib.stream_of(x.device)),
+        "rms_norm_gated",
+    )
+    return out
+
+
+def readout_fused(states, q, gate, weight, *, scale: float, eps: float, softcap: float = 2.0,
+                  gate_kind: str = "softcap_silu", slot_idx=None):
+    """Decode readout of one query token per sequence fused with the
+    epilogue: ``r = bf16(scale * q . S)`` then ``MemTRMSNormGated(r, gate)``.
+
+    ``states`` [slots,H,K,V] fp32 (``slot_idx`` [B] int32 picks each
+    sequence's slot, default ``b``), ``q`` [B,H,K] bf16 (l2-normalised by the
+    caller), ``gate`` [B,H,V] bf16, ``weight`` [V] bf16.  Returns [B, H*V] bf16.
+    """
+    lib = _lib.load()
+    _lib.require_gpu(states, q, gate, weight)
+    if gate_kind not in _GATES:
+        raise ValueError(f"gate_kind must be one of {sorted(_GATES)}")
+    B, H, K = q.shape
+    V = states.shape[-1]
+    if states.ndim != 4 or states.shape[1] != H or states.shape[2] != K or states.dtype != torch.float32:
+        raise ValueError("states must be fp32 [slots, H, K, V]")
+    if gate.shape != (B, H, V) or weight.shape != (V,):
+        raise ValueError("gate must be [B, H, V] and weight [V]")
+    if slot_idx is None and states.shape[0] < B:
+        raise ValueError("fewer state slots than sequences")
+    if slot_idx is not None:
+        if not isinstance(slot_idx, torch.Tensor) or not slot_idx.is_cuda:
+            # host indices are range-checked before they reach the kernel
+            host = torch.as_tensor(slot_idx, dtype=torch.int64).reshape(-1)
+            if host.numel() != B or (B and (int(host.min()) < 0 or int(host.max()) >= states.shape[0])):
+                raise ValueError("slot_idx must hold B indices into the state slots")
+            slot_idx = host.to(device=q.device, dtype=torch.int32)
+        if slot_idx.dtype != torch.int32 or slot_idx.shape != (B,):
+            raise ValueError("slot_idx must be int32 [B]")
+    states, q, gate, weight, slot_idx = _contig(states, q, gate, weight, slot_idx)
+    out = torch.empty(B, H * V, dtype=torch.bfloat16, device=q.device)
+    _lib.check(
+        lib.memt_gdn2_readout_fused(states.data_ptr(), _lib.ptr(slot_idx), q.data_ptr(), gate.data_ptr(),
+                                    weight.data_ptr(), out.data_ptr(), B, H, K, V, float(scale), float(eps),
+                                    float(softcap), _GATES[gate_kind], _lib.stream_of(q.device)),
+        "readout_fused",
+    )
+    return out

@@ -1,0 +1,164 @@
+"""GPU parity of the chunked GDN-2 update (WY stage + state scan + outputs)
+against the CPU oracle: the fp64 token recurrence on small cases, the fp64
+chunked form (a different algorithm, pinned equal to the recurrence) on the
+full-size workload's heads."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn2 as O
+from gpu_util import bf, host, to_dev
+
+import memt_gdn2
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3  # max|x - ref| / max|ref| (bf16 outputs: beyond one bf16 ulp of ref)
+
+
+def _dev_inputs(inp, dev):
+    return (bf(inp["q"], dev), bf(inp["k"], dev), bf(inp["v"], dev), to_dev(inp["g"], dev),
+            to_dev(inp["beta"], dev), to_dev(inp["h0"], dev))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [1, 63, 64, 200])
+def test_causal_vs_recurrent(dev, T, D):
+    print(f"causal T={T} D={D}", flush=True)
+    H = 2
+    inp = O.synth_inputs(T, H, D, D, seed=100 + T + D, h0_std=0.05)
+    q, k, v, g, beta, h0 = _dev_inputs(inp, dev)
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, initial_state=h0, out_mode="causal")
+    o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], h0=inp["h0"])
+    assert O.max_rel_err(host(ht), h_ref) <= TOL
+    assert O.parity_err(host(o), o_ref, out_bf16=True) <= TOL
+
+
+def test_varlen_bf16_beta_erase_events(dev):
+    """Packed sequences, bf16 write gate, channel erase gate, write events."""
+    rng = np.random.default_rng(9)
+    T, H, D = 300, 3, 64
+    cu = [0, 37, 37 + 130, T]
+    inp = O.synth_inputs(T, H, D, D, seed=9, h0_std=0.1, n_seq=3)
+    beta = O.bf16_round(inp["beta"])
+    b = O.bf16_round(rng.uniform(0.3, 1.0, (1, T, H, D)).astype(np.float32))
+    q, k, v, g, _, h0 = _dev_inputs(inp, dev)
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, bf(beta, dev), b=bf(b, dev), initial_state=h0, cu_seqlens=cu,
+                                 out_mode="causal", chunk_tokens=96)
+    o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], beta, b=b, h0=inp["h0"],
+                                    cu_seqlens=cu)
+    assert O.max_rel_err(host(ht), h_ref) <= TOL
+    assert O.parity_err(host(o), o_ref, out_bf16=True) <= TOL
+
+
+def test_token_memory_packed(dev):
+    """The plugin drop-in: commits from write_states, reads read_states."""
+    T, H, D = 260, 2, 128
+    lengths = [130, 1, 129]
+    inp = O.synth_inputs(T, H, D, D, seed=21, h0_std=0.05, n_seq=3)
+    rs = (np.random.default_rng(22).standard_normal((3, H, D, D)) * 0.05).astype(np.float32)
+    q, k, v, g, _, ws = _dev_inputs(inp, dev)
+    beta = O.bf16_round(inp["beta"])
+    read, final = memt_gdn2.token_memory_packed(q, k, v, g, bf(beta, dev), to_dev(rs, dev), ws, erase=None,
+                                                lengths=lengths, scale=D ** -0.5, chunk_tokens=64)
+    r_ref, f_ref = O.token_memory_packed(inp["q"], inp["k"], inp["v"], inp["g"], beta, rs, inp["h0"], erase=None,
+                                         lengths=lengths, scale=D ** -0.5, chunk_tokens=64)
+    assert O.max_rel_err(host(final), f_ref) <= TOL
+    assert O.parity_err(host(read), r_ref, out_bf16=True) <= TOL
+
+
+def test_snapshot_mode_and_no_initial_state(dev):
+    T, H, D = 100, 2, 64
+    inp = O.synth_inputs(T, H, D, D, seed=31)
+    q, k, v, g, beta, _ = _dev_inputs(inp, dev)
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, out_mode="snapshot")
+    o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], out_mode="snapshot")
+    assert O.max_rel_err(host(ht), h_ref) <= TOL
+    assert np.all(host(o) == 0.0) and np.all(o_ref == 0.0)
+    o2, ht2 = memt_gdn2.chunk_gdn2(q, k, v, g, beta, out_mode="none")
+    assert o2 is None and torch.equal(ht2, ht)
+
+
+def test_wy_stage_reference_layout(dev):
+    """chunk_gdn2_fwd_intra outputs vs the oracle's per-chunk WY quantities."""
+    T, H, D = 150, 2, 64
+    inp = O.synth_inputs(T, H, D, D, seed=41)
+    gk = O.chunk_local_cumsum(inp["g"], 64, scale=O.RCP_LN2).astype(np.float32)
+    q, k, v, _, beta, _ = _dev_inputs(inp, dev)
+    scale = D ** -0.5
+    w, u, qg, kg, Aqk, Akk = memt_gdn2.chunk_gdn2_fwd_intra(q, k, v, to_dev(gk, dev), None, beta, scale,
+                                                            disable_recompute=True)
+    w, u, qg, kg, Aqk, Akk = (host(x) for x in (w, u, qg, kg, Aqk, Akk))
+    for h in range(H):
+        for c0 in range(0, T, 64):
+            c1 = min(c0 + 64, T)
+            n = c1 - c0
+            wy = O.wy_chunk(inp["k"][0, c0:c1, h], inp["v"][0, c0:c1, h], gk[0, c0:c1, h].astype(np.float64),
+                            inp["beta"][0, c0:c1, h])
+            assert O.parity_err(Akk[0, c0:c1, h, :n], wy["A"], out_bf16=True) <= TOL
+            assert O.parity_err(w[0, c0:c1, h], wy["W"], out_bf16=True) <= TOL
+            assert O.parity_err(u[0, c0:c1, h], wy["U"], out_bf16=True) <= TOL
+            assert O.parity_err(kg[0, c0:c1, h], wy["kg"], out_bf16=True) <= TOL
+            qh = inp["q"][0, c0:c1, h].astype(np.float64)
+            assert O.parity_err(qg[0, c0:c1, h], qh * wy["gam"], out_bf16=True) <= TOL
+            kh = inp["k"][0, c0:c1, h].astype(np.float64)
+            gh = gk[0, c0:c1, h].astype(np.float64)
+            ref_aqk = np.zeros((n, n))
+            for i in range(n):
+                for j in range(i + 1):
+                    ref_aqk[i, j] = scale * np.sum(qh[i] * kh[j] * np.exp2(gh[i] - gh[j]))
+            assert O.parity_err(Aqk[0, c0:c1, h, :n], ref_aqk, out_bf16=True) <= TOL
+
+
+def test_fwd_h_from_reference_layout(dev):
+    """memt_gdn2_fwd_h on bf16 WY tensors vs the oracle scan of the same
+    tensors: snapshots at block starts, uncommitted events, final states."""
+    T, H, D = 260, 2, 64
+    inp = O.synth_inputs(T, H, D, D, seed=51, h0_std=0.05, n_seq=2)
+    samples = [0, 120, 260]
+    events = [0, 64, 120, 200, 260]
+    commit = [1, 0, 1, 1]
+    gk = O.chunk_local_cumsum(inp["g"], 64, scale=O.RCP_LN2, cu_seqlens=events)
+    oplan = O.build_chunk_plan(samples, samples, event_slice=events, commit_mask=commit)
+    w, u, kg = (np.zeros_like(inp[n]) for n in ("k", "v", "k"))
+    for h in range(H):
+        for c in range(oplan.num_chunk):
+            c0 = int(oplan.chunk_tok0[c])
+            c1 = c0 + int(oplan.chunk_len[c])
+            wy = O.wy_chunk(inp["k"][0, c0:c1, h], inp["v"][0, c0:c1, h], gk[0, c0:c1, h], inp["beta"][0, c0:c1, h])
+            w[0, c0:c1, h], u[0, c0:c1, h], kg[0, c0:c1, h] = wy["W"], wy["U"], wy["kg"]
+    w, u, kg = (O.bf16_round(x) for x in (w, u, kg))
+    gk32 = gk.astype(np.float32)
+    plan = memt_gdn2.build_chunk_plan(samples, samples, event_slice=events, commit_mask=commit, device=dev)
+    snaps, final = memt_gdn2.memt_gdn2_fwd_h(bf(kg, dev), bf(w, dev), bf(u, dev), to_dev(gk32, dev), plan,
+                                             initial_state=to_dev(inp["h0"], dev))
+    s_ref, f_ref = O.state_scan(kg, w, u, gk32, oplan, h0=inp["h0"])
+    assert O.max_rel_err(host(final), f_ref) <= TOL
+    assert np.array_equal(host(snaps), s_ref.astype(np.float32))
+
+
+def test_read_fwd(dev):
+    T, H, D = 150, 2, 128
+    lengths = [50, 100]
+    rng = np.random.default_rng(61)
+    q = O.bf16_round(O.l2norm(rng.standard_normal((1, T, H, D)).astype(np.float32))[0])
+    S = (rng.standard_normal((2, H, D, D)) * 0.1).astype(np.float32)
+    out = memt_gdn2.snapshot_read(bf(q, dev), to_dev(S, dev), lengths, D ** -0.5)
+    ref = O.snapshot_read(q, S, lengths, D ** -0.5)
+    assert O.parity_err(host(out), ref, out_bf16=True) <= TOL
+
+
+def test_full_size_workload_heads(dev):
+    """B=1, H=16, T=8192, d=128, chunk 64: the final state of every head and the
+    causal output of four heads vs the fp64 chunked oracle on those heads."""
+    T, H, D = 8192, 16, 128
+    inp = O.synth_inputs(T, H, D, D, seed=20261202, h0_std=0.02)
+    q, k, v, g, beta, h0 = _dev_inputs(inp, dev)
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, initial_state=h0, out_mode="causal")
+    o, ht = host(o), host(ht)
+    assert np.all(np.isfinite(o)) and np.all(np.isfinite(ht))
+    hs = [0, 5, 10, 15]
+    sub = {n: a[:, :, hs] for n, a in inp.items() if n != "h0"}
+    o_ref, h_ref = O.chunked_gdn2(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"], h0=inp["h0"][:, hs])
+    assert O.max_rel_err(ht[:, hs], h_ref) <= TOL
+    assert O.parity_err(o[:, :, hs], o_ref, out_bf16=True) <= TOL
