@@ -73,12 +73,57 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   write_S_lds();
   __syncthreads();
 
-  const int c_begin = a.seq_chunk_offsets[n], c_end = a.seq_chunk_offsets[n + 1];
-  for (int c = c_begin; c < c_end; ++c) {
+  // Everything a chunk needs from global memory, loaded one chunk ahead so the
+  // loads of chunk c+1 are in flight while chunk c computes.
+  struct Frag {
+    bf16x8 w[K / 32];
+    bf16x8 qg[CAUSAL ? K / 32 : 1];
+    f16x4 u[CT];
+    f32x4 d[RT];
+    f16x8 kg[RT][2];
+    f16x8 aq[CAUSAL ? 2 : 1];
+    int flags, block, tok0, len;
+  };
+  auto load_frag = [&](int c, Frag& f) {
     const size_t unit = (size_t)c * H + h;
-    const int flags = a.chunk_flags ? a.chunk_flags[c] : MEMT_GDN2_CHUNK_COMMIT;
-    if (a.snaps != nullptr && (flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
-      const size_t soff = ((size_t)a.chunk_block_ids[c] * H + h) * K * V;
+    const __bf16* Wp = a.in.W + unit * (size_t)(C * K);
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+      const size_t fo = ((size_t)(w * (K / 32) + s) * 64 + lane) * 8;
+      f.w[s] = *(const bf16x8*)(Wp + fo);
+      if constexpr (CAUSAL) f.qg[s] = *(const bf16x8*)(a.in.qg + unit * (size_t)(C * K) + fo);
+    }
+    const _Float16* Up = a.in.U + unit * (size_t)(C * V);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+      f.u[ct] = *(const f16x4*)(Up + ((size_t)(w * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
+    const float* dp = a.in.decay + unit * K;
+    const _Float16* Kp = a.in.kgT + unit * (size_t)(C * K);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int rtile = w * RT + rt;
+      f.d[rt] = *(const f32x4*)(dp + 16 * rtile + 4 * lg);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) f.kg[rt][s] = *(const f16x8*)(Kp + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
+    }
+    if constexpr (CAUSAL) {
+      const _Float16* Ap = a.in.Aqk + unit * (size_t)(C * C);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) f.aq[s] = *(const f16x8*)(Ap + ((size_t)(w * 2 + s) * 64 + lane) * 8);
+      f.tok0 = a.chunk_tok0[c];
+      f.len = a.chunk_len[c];
+    }
+    f.flags = a.chunk_flags ? a.chunk_flags[c] : MEMT_GDN2_CHUNK_COMMIT;
+    f.block = (a.snaps != nullptr && (f.flags & MEMT_GDN2_CHUNK_BLOCK_START)) ? a.chunk_block_ids[c] : -1;
+  };
+
+  const int c_begin = a.seq_chunk_offsets[n], c_end = a.seq_chunk_offsets[n + 1];
+  Frag cur, nxt;
+  if (c_begin < c_end) load_frag(c_begin, cur);
+  for (int c = c_begin; c < c_end; ++c) {
+    if (c + 1 < c_end) load_frag(c + 1, nxt);
+    if (cur.block >= 0) {
+      const size_t soff = ((size_t)cur.block * H + h) * K * V;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -97,81 +142,67 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
       acc[ct] = zero4();
       if constexpr (CAUSAL) acco[ct] = zero4();
     }
-    const __bf16* Wp = a.in.W + unit * (size_t)(C * K);
-    const __bf16* Qp = CAUSAL ? a.in.qg + unit * (size_t)(C * K) : nullptr;
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) {
-      const size_t fo = ((size_t)(w * (K / 32) + s) * 64 + lane) * 8;
-      const bf16x8 wa = *(const bf16x8*)(Wp + fo);
-      bf16x8 qa;
-      if constexpr (CAUSAL) qa = *(const bf16x8*)(Qp + fo);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         const bf16x8 sb = *(const bf16x8*)(&S_lds[(16 * ct + lr) * SKP + 32 * s + 8 * lg]);
-        acc[ct] = mfma_bf16(wa, sb, acc[ct]);
-        if constexpr (CAUSAL) acco[ct] = mfma_bf16(qa, sb, acco[ct]);
+        acc[ct] = mfma_bf16(cur.w[s], sb, acc[ct]);
+        if constexpr (CAUSAL) acco[ct] = mfma_bf16(cur.qg[s], sb, acco[ct]);
       }
     }
-    const _Float16* Up = a.in.U + unit * (size_t)(C * V);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      const f16x4 u4 = *(const f16x4*)(Up + ((size_t)(w * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
       f16x4 vn;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)u4[e] - acc[ct][e]);
+      for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)cur.u[ct][e] - acc[ct][e]);
       *(f16x4*)(&Vn_lds[(16 * ct + lr) * VNP + 16 * w + 4 * lg]) = vn;
     }
     __syncthreads();
 
     // ---- phase 2: state update and causal output ----
-    if (flags & MEMT_GDN2_CHUNK_COMMIT) {
-      const float* dp = a.in.decay + unit * K;
-      const _Float16* Kp = a.in.kgT + unit * (size_t)(C * K);
+    if (cur.flags & MEMT_GDN2_CHUNK_COMMIT) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const int rtile = w * RT + rt;
-        const f32x4 d = *(const f32x4*)(dp + 16 * rtile + 4 * lg);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) S[rt][ct][e] *= d[e];
+          for (int e = 0; e < 4; ++e) S[rt][ct][e] *= cur.d[rt][e];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const f16x8 ka = *(const f16x8*)(Kp + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) {
             const f16x8 vb = *(const f16x8*)(&Vn_lds[(16 * ct + lr) * VNP + 32 * s + 8 * lg]);
-            S[rt][ct] = mfma_f16(ka, vb, S[rt][ct]);
+            S[rt][ct] = mfma_f16(cur.kg[rt][s], vb, S[rt][ct]);
           }
         }
       }
     }
     if constexpr (CAUSAL) {
-      const _Float16* Ap = a.in.Aqk + unit * (size_t)(C * C);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acco[ct][e] *= a.scale;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const f16x8 aq = *(const f16x8*)(Ap + ((size_t)(w * 2 + s) * 64 + lane) * 8);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
           const f16x8 vb = *(const f16x8*)(&Vn_lds[(16 * ct + lr) * VNP + 32 * s + 8 * lg]);
-          acco[ct] = mfma_f16(aq, vb, acco[ct]);
+          acco[ct] = mfma_f16(cur.aq[s], vb, acco[ct]);
         }
       }
-      const int tok0 = a.chunk_tok0[c], len = a.chunk_len[c];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int t = 16 * w + 4 * lg + e;
-          if (t < len) a.o[((size_t)(tok0 + t) * H + h) * V + v0 + 16 * ct + lr] = (__bf16)acco[ct][e];
+          if (t < cur.len)
+            a.o[((size_t)(cur.tok0 + t) * H + h) * V + v0 + 16 * ct + lr] = (__bf16)acco[ct][e];
         }
     }
     write_S_lds();
     __syncthreads();
+    cur = nxt;
   }
 
   if (a.ht != nullptr) {

@@ -49,36 +49,89 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
   const int len = a.chunk_len[chunk];
   const size_t unit = (size_t)chunk * H + h;
 
-  // ---- phase 1: stage k / q / b, zero A_s, chunk-local decay cumsum --------
+  // ---- phase 1: issue every global load of the chunk at once (k, q, b, g and
+  //      the v / beta operands of phase 4), stage k / q / b, decay cumsum ----
   constexpr int K8 = K / 8;
-  for (int idx = tid; idx < C * K8; idx += 256) {
+  constexpr int V8 = V / 8;
+  constexpr int NKL = C * K8 / 256;  // 16-byte k/q/b loads per thread
+  constexpr int NVL = C * V8 / 256;  // 8-element v/beta groups per thread
+  static_assert(NKL * 256 == C * K8 && NVL * 256 == C * V8, "load tiling");
+  constexpr int TPC = (256 / K) < 1 ? 1 : (256 / K);  // threads per channel
+  constexpr int SEG = C / TPC;
+  u32x4 kv[NKL], qv[CAUSAL ? NKL : 1], bv[HAS_B ? NKL : 1];
+#pragma unroll
+  for (int i = 0; i < NKL; ++i) {
+    const int idx = tid + 256 * i;
     const int t = idx / K8, c8 = (idx % K8) * 8;
     const size_t goff = ((size_t)(tok0 + t) * H + h) * K + c8;
-    u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u}, bv = {0u, 0u, 0u, 0u};
+    kv[i] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (CAUSAL) qv[i] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (HAS_B) bv[i] = u32x4{0u, 0u, 0u, 0u};
     if (t < len) {
-      kv = *(const u32x4*)(a.k + goff);
-      if constexpr (CAUSAL) qv = *(const u32x4*)(a.q + goff);
-      if constexpr (HAS_B) bv = *(const u32x4*)(a.b + goff);
+      kv[i] = *(const u32x4*)(a.k + goff);
+      if constexpr (CAUSAL) qv[i] = *(const u32x4*)(a.q + goff);
+      if constexpr (HAS_B) bv[i] = *(const u32x4*)(a.b + goff);
     }
-    *(u32x4*)(&k_s[t * KB + c8]) = kv;
-    if constexpr (CAUSAL) *(u32x4*)(&q_s[t * KB + c8]) = qv;
-    if constexpr (HAS_B) *(u32x4*)(&b_s[t * KB + c8]) = bv;
+  }
+  float gv[SEG];
+  {
+    const int c = tid % K, seg = tid / K;
+#pragma unroll
+    for (int i = 0; i < SEG; ++i) {
+      const int t = seg * SEG + i;
+      gv[i] = (tid < K * TPC && t < len) ? a.g[((size_t)(tok0 + t) * H + h) * K + c] : 0.f;
+    }
+  }
+  bf16x8 vreg[NVL];
+  float breg[NVL][8];
+#pragma unroll
+  for (int i = 0; i < NVL; ++i) {
+    const int idx = tid + 256 * i;
+    const int t = idx / V8, c8 = (idx % V8) * 8;
+    const size_t goff = ((size_t)(tok0 + t) * H + h) * V + c8;
+    if (t < len) {
+      vreg[i] = *(const bf16x8*)(a.v + goff);
+      if constexpr (sizeof(BetaT) == 4) {
+        const f32x4 b0 = *(const f32x4*)((const float*)a.beta + goff);
+        const f32x4 b1 = *(const f32x4*)((const float*)a.beta + goff + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          breg[i][e] = b0[e];
+          breg[i][4 + e] = b1[e];
+        }
+      } else {
+        const bf16x8 bb = *(const bf16x8*)((const __bf16*)a.beta + goff);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) breg[i][e] = (float)bb[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vreg[i][e] = (__bf16)0.f;
+        breg[i][e] = 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NKL; ++i) {
+    const int idx = tid + 256 * i;
+    const int t = idx / K8, c8 = (idx % K8) * 8;
+    *(u32x4*)(&k_s[t * KB + c8]) = kv[i];
+    if constexpr (CAUSAL) *(u32x4*)(&q_s[t * KB + c8]) = qv[i];
+    if constexpr (HAS_B) *(u32x4*)(&b_s[t * KB + c8]) = bv[i];
   }
   for (int idx = tid; idx < C * LP; idx += 256) A_s[idx] = 0.f;
 
-  constexpr int TPC = (256 / K) < 1 ? 1 : (256 / K);  // threads per channel
-  constexpr int SEG = C / TPC;
   if (tid < K * TPC) {
     const int c = tid % K, seg = tid / K;
     float run = 0.f;
-#pragma unroll 8
+#pragma unroll
     for (int i = 0; i < SEG; ++i) {
       const int t = seg * SEG + i;
-      const float x = (t < len) ? a.g[((size_t)(tok0 + t) * H + h) * K + c] : 0.f;
       if constexpr (G_CUM) {
-        gk_s[t * KP + c] = x;
+        gk_s[t * KP + c] = gv[i];
       } else {
-        run += x;
+        run += gv[i];
         gk_s[t * KP + c] = run;
       }
     }
@@ -90,6 +143,7 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
     if constexpr (!G_CUM) {
       float off = 0.f;
       for (int s2 = 0; s2 < seg; ++s2) off += tot_s[s2 * K + c];
+#pragma unroll
       for (int i = 0; i < SEG; ++i) {
         const int t = seg * SEG + i;
         gk_s[t * KP + c] = (gk_s[t * KP + c] + off) * kRcpLn2;
@@ -97,6 +151,7 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
     } else {
       // padding rows repeat the last valid cumulative decay
       const float last = gk_s[(len - 1) * KP + c];
+#pragma unroll
       for (int i = 0; i < SEG; ++i) {
         const int t = seg * SEG + i;
         if (t >= len) gk_s[t * KP + c] = last;
@@ -265,24 +320,12 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
   // ---- phase 4: xu = beta * v (f16, column-major, aliases gk_s) and the
   //      off-diagonal inverse blocks -----------------------------------------
   _Float16* xu_s = (_Float16*)gk_s;
-  {
-    constexpr int V8 = V / 8;
-    const BetaT* beta = (const BetaT*)a.beta;
-    for (int idx = tid; idx < C * V8; idx += 256) {
-      const int t = idx / V8, c8 = (idx % V8) * 8;
-      float vb[8];
-      if (t < len) {
-        const size_t goff = ((size_t)(tok0 + t) * H + h) * V + c8;
-        const bf16x8 vv = *(const bf16x8*)(a.v + goff);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vb[e] = (float)vv[e] * load_as_f32<BetaT>(beta + goff + e);
-      } else {
+  for (int i = 0; i < NVL; ++i) {
+    const int idx = tid + 256 * i;
+    const int t = idx / V8, c8 = (idx % V8) * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vb[e] = 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xu_s[(c8 + e) * CB + t] = (_Float16)vb[e];
-    }
+    for (int e = 0; e < 8; ++e) xu_s[(c8 + e) * CB + t] = (_Float16)((float)vreg[i][e] * breg[i][e]);
   }
   // A_{I+d, I} for d = 1, 2, 3 (one 16x16 block per wave per stage).
 #pragma unroll
