@@ -27,6 +27,18 @@ __host__ __device__ __forceinline__ int afrag_index(int row, int col, int red) {
   const int lane = (row & 15) + ((col >> 3) & 3) * 16;
   return ((rt * (red >> 5) + s) * 64 + lane) * 8 + (col & 7);
 }
+// P-frag: an A-frag whose reduction index is permuted so that it pairs with a
+// B operand assembled from two C fragments (rows 4*(lane/16)+0..3 of 16-row
+// tiles 2s and 2s+1).  Lane l's 8 elements at step s are
+//   X[16*rt + l%16][32*s + 4*(l/16) + e]        e = 0..3
+//   X[16*rt + l%16][32*s + 16 + 4*(l/16) + e]   e = 0..3
+// so accumulators of one product feed the next without an LDS round trip.
+__host__ __device__ __forceinline__ int pfrag_index(int row, int col, int red) {
+  const int rt = row >> 4, s = col >> 5, within = col & 31;
+  const int half = within >> 4, lg = (within & 15) >> 2, e = within & 3;
+  const int lane = (row & 15) + lg * 16;
+  return ((rt * (red >> 5) + s) * 64 + lane) * 8 + half * 4 + e;
+}
 __host__ __device__ __forceinline__ int cfrag_index(int row, int col, int n) {
   const int rt = row >> 4, ct = col >> 4;
   const int lane = (col & 15) + ((row >> 2) & 3) * 16;
@@ -36,12 +48,12 @@ __host__ __device__ __forceinline__ int cfrag_index(int row, int col, int n) {
 __host__ __device__ __forceinline__ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Per-(chunk, head) records of the WY stage, unit u = chunk * H + head.
-//   W     bf16 [64 x K]  A-frag (rows = tokens, red = K)       erase path
-//   kgT   f16  [K x 64]  A-frag of kg^T (rows = K, red = tokens) value path
+//   W     bf16 [64 x K]  P-frag (rows = tokens, red = K)       erase path
+//   kgT   f16  [K x 64]  P-frag of kg^T (rows = K, red = tokens) value path
 //   U     f16  [64 x V]  C-frag                                 value path
 //   decay f32  [K]       2^{gk_last}
-//   qg    bf16 [64 x K]  A-frag, q * 2^{gk}                     (causal output)
-//   Aqk   f16  [64 x 64] A-frag, scale * causal scores          (causal output)
+//   qg    bf16 [64 x K]  P-frag, q * 2^{gk}                     (causal output)
+//   Aqk   f16  [64 x 64] P-frag, scale * causal scores          (causal output)
 struct WyBuffers {
   __bf16* W;
   _Float16* kgT;

@@ -7,6 +7,8 @@
 //                                                           FLA/ops/gdn2/chunk_intra.py:233-299)
 //   A     = (I + L)^-1                                     (chunk_intra.py:326-395)
 //   W     = A (b k 2^gk),  U = A (beta v)                  (FLA/ops/gdn2/wy_fast.py:92-142)
+// Outputs go to the workspace as MFMA operand fragments of the state scan
+// (P-frags for W, qg, kg^T and Aqk; a C-frag for U).
 //   kg    = k 2^(gk_last - gk), decay = 2^gk_last          (wy_fast.py:125-139)
 //   Aqk   = scale * sum_c q_ic k_jc 2^(gk_ic - gk_jc), j <= i, qg = q 2^gk   (causal output only)
 //
@@ -277,27 +279,30 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
     for (int i = 0; i < 16; ++i) A_s[(n + i) * LP + n + j] = x[i];
   }
   {
-    // kg^T A-frag (rows = K channel, red = tokens) to global, xw (col-major) to LDS.
+    // kg^T P-frag (rows = K channel, red = tokens) to global, xw (col-major) to LDS.
     _Float16* kg_out = a.out.kgT + unit * (size_t)(C * K);
     for (int grp = tid; grp < K * C / 8; grp += 256) {
       const int lane_f = grp & 63, rs = grp >> 6;  // rs = rt * 2 + s
       const int s = rs & 1, rt = rs >> 1;
       const int m = 16 * rt + (lane_f & 15);
-      const int t0 = 32 * s + 8 * (lane_f >> 4);
       const float glast = gk_s[(C - 1) * KP + m];
       f16x8 kgv;
-      bf16x8 xwv;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = t0 + e;
-        const float gt = gk_s[t * KP + m];
-        const float kt = (float)k_s[t * KB + m];
-        const float bk = HAS_B ? kt * (float)b_s[t * KB + m] : kt;
-        kgv[e] = (_Float16)(kt * fast_exp2(glast - gt));
-        xwv[e] = (__bf16)(bk * fast_exp2(gt));
+      for (int half = 0; half < 2; ++half) {
+        const int t0 = 32 * s + 16 * half + 4 * (lane_f >> 4);
+        bf16x4 xwv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = t0 + e;
+          const float gt = gk_s[t * KP + m];
+          const float kt = (float)k_s[t * KB + m];
+          const float bk = HAS_B ? kt * (float)b_s[t * KB + m] : kt;
+          kgv[4 * half + e] = (_Float16)(kt * fast_exp2(glast - gt));
+          xwv[e] = (__bf16)(bk * fast_exp2(gt));
+        }
+        *(bf16x4*)(&xw_s[m * CB + t0]) = xwv;
       }
       *(f16x8*)(kg_out + (size_t)grp * 8) = kgv;
-      *(bf16x8*)(&xw_s[m * CB + t0]) = xwv;
     }
     for (int c = tid; c < K; c += 256) a.out.decay[unit * K + c] = fast_exp2(gk_s[(C - 1) * KP + c]);
     if constexpr (CAUSAL) {
@@ -306,11 +311,14 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
         const int lane_f = grp & 63, rs = grp >> 6;  // rs = rt * (K/32) + s
         const int s = rs % (K / 32), rt = rs / (K / 32);
         const int t = 16 * rt + (lane_f & 15);
-        const int c0 = 32 * s + 8 * (lane_f >> 4);
         bf16x8 qv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          qv[e] = (__bf16)((float)q_s[t * KB + c0 + e] * fast_exp2(gk_s[t * KP + c0 + e]));
+        for (int half = 0; half < 2; ++half) {
+          const int c0 = 32 * s + 16 * half + 4 * (lane_f >> 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            qv[4 * half + e] = (__bf16)((float)q_s[t * KB + c0 + e] * fast_exp2(gk_s[t * KP + c0 + e]));
+        }
         *(bf16x8*)(qg_out + (size_t)grp * 8) = qv;
       }
     }
@@ -413,8 +421,10 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
       const int lane_f = grp & 63, rs = grp >> 6;
       const int s = rs % (K / 32), rt = rs / (K / 32);
       const int t = 16 * rt + (lane_f & 15);
-      const int c0 = 32 * s + 8 * (lane_f >> 4);
-      *(bf16x8*)(W_out + (size_t)grp * 8) = *(const bf16x8*)(&Wst[t * KB + c0]);
+      const int c0 = 32 * s + 4 * (lane_f >> 4);
+      const bf16x4 lo = *(const bf16x4*)(&Wst[t * KB + c0]);
+      const bf16x4 hi = *(const bf16x4*)(&Wst[t * KB + c0 + 16]);
+      *(bf16x8*)(W_out + (size_t)grp * 8) = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
     if constexpr (CAUSAL) {
       _Float16* Aqk_out = a.out.Aqk + unit * (size_t)(C * C);
@@ -422,10 +432,13 @@ __global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
         const int lane_f = grp & 63, rs = grp >> 6;
         const int s = rs & 1, rt = rs >> 1;
         const int t = 16 * rt + (lane_f & 15);
-        const int j0 = 32 * s + 8 * (lane_f >> 4);
+        const int j0 = 32 * s + 4 * (lane_f >> 4);
         f16x8 av;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) av[e] = (_Float16)Aqk_s[t * LP + j0 + e];
+        for (int e = 0; e < 4; ++e) {
+          av[e] = (_Float16)Aqk_s[t * LP + j0 + e];
+          av[4 + e] = (_Float16)Aqk_s[t * LP + j0 + 16 + e];
+        }
         *(f16x8*)(Aqk_out + (size_t)grp * 8) = av;
       }
     }
