@@ -51,10 +51,34 @@ __device__ __forceinline__ float load_as_f32<float>(const float* p) { return *p;
 template <>
 __device__ __forceinline__ float load_as_f32<__bf16>(const __bf16* p) { return (float)*p; }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (vmcnt(0)).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// x from lane (i - N) of the same 16-lane row, 0 for the first N lanes of a row.
+template <int N>
+__device__ __forceinline__ float dpp_row_shr(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x110 + N, 0xF, 0xF, true));
+}
+// Inclusive prefix sum over the 16 lanes of each row.
+__device__ __forceinline__ float row_inclusive_scan(float x) {
+  x += dpp_row_shr<1>(x);
+  x += dpp_row_shr<2>(x);
+  x += dpp_row_shr<4>(x);
+  x += dpp_row_shr<8>(x);
+  return x;
+}
+
 // Wave64 sum reduction (all lanes receive the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
 }
 

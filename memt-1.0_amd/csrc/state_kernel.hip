@@ -26,10 +26,6 @@
 namespace memt {
 namespace {
 
-// Workgroup barrier that orders LDS only.  __syncthreads() also fences global
-// memory, which would wait for every outstanding prefetch load.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 template <int K, int V, int BV, bool CAUSAL>
 struct ScanFrag {
   static constexpr int KS = K / 32;

@@ -1,4 +1,4 @@
-// WY stage of the chunked GDN-2 update, one workgroup per (chunk, head).
+// WY stage of the chunked GDN-2 update, one workgroup (4 waves) per (chunk, head).
 //
 // For a chunk of C <= 64 tokens (rows past the chunk end are zero padded):
 //   gk    = 1/ln2 * cumsum_chunk(g)                       (FLA/ops/utils/cumsum.py:116-133)
@@ -7,446 +7,517 @@
 //                                                           FLA/ops/gdn2/chunk_intra.py:233-299)
 //   A     = (I + L)^-1                                     (chunk_intra.py:326-395)
 //   W     = A (b k 2^gk),  U = A (beta v)                  (FLA/ops/gdn2/wy_fast.py:92-142)
-// Outputs go to the workspace as MFMA operand fragments of the state scan
-// (P-frags for W, qg, kg^T and Aqk; a C-frag for U).
 //   kg    = k 2^(gk_last - gk), decay = 2^gk_last          (wy_fast.py:125-139)
 //   Aqk   = scale * sum_c q_ic k_jc 2^(gk_ic - gk_jc), j <= i, qg = q 2^gk   (causal output only)
+// Outputs go to the workspace as MFMA operand fragments of the state scan
+// (P-frags for W, qg, kg^T and Aqk; a C-frag for U).
 //
+// Register layout.  Wave w owns tokens [16w, 16w+16).  Lane l holds token
+// 16w + l%16 and, for channel step s, the 8 channels
+//   slot j -> channel 32 s + 16 (j / 4) + 4 (l / 16) + j % 4      (P-frag order)
+// of every per-token input.  Loaded once in that order, the registers serve
+// directly as MFMA A operands of row-block products, as B operands of the
+// transposed products, and as P-frag records of the outputs.
+//
+// Steps:
+//   cumsum    16-lane DPP row scans inside each 16-token block, block totals through LDS.
+//   factors   fa = 2^(gk - gk_start) <= 1 and 1/fa, with gk_start the cumulative decay at
+//             the first token of the lane's block; per-channel block factors in LDS.
+//   L, Aqk    16x16 tiles, computed transposed so that each lane holds one row.
+//             Diagonal tiles: split-bf16 MFMA (hi*hi + hi*lo + lo*hi) of (b k fa) and
+//             (k / fa): fp32 range and ~2^-16 relative precision.  Off-diagonal tiles
+//             (J < I): fp16 MFMA of (b k fa) and k 2^(gk_start(I) - gk) <= 1, the latter
+//             built by wave J.  A block whose in-block decay exceeds 2^96 forms its
+//             diagonal tile from exact pairwise factors instead (wave-local shuffles).
+//   inverse   A_II by row-wise substitution (fp32), then
+//             A_IJ = -A_II sum_{J<=M<I} L_IM A_MJ with fp32 MFMA, through LDS.
+//   W, U      bf16 / fp16 MFMA against column-major xw / xu tiles in LDS, staged by an
+//             exact identity-matrix MFMA transpose of each wave's rows.
 // Precision: the erase path (W, b k 2^gk) is bf16; the value path (beta v, A, U,
-// kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.  The diagonal
-// 16x16 blocks of L use fp32 MFMA with factors re-centred at the block start;
-// a block whose in-block decay exceeds 2^64 takes an exact pairwise path.
-// Off-diagonal blocks are re-centred at the row block start, so both operand
-// factors are <= 1 and fp16 MFMA is safe.  The inverse is formed block-wise:
-// forward substitution on the diagonal blocks, then
-// A_IJ = -A_II sum_{J<=M<I} L_IM A_MJ with fp32 MFMA.
+// kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.
+// LDS stays under 80 KB at d = 128, so two workgroups share a CU.
 #include "gdn2_internal.h"
 
 namespace memt {
 namespace {
 
-template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT>
-__global__ __launch_bounds__(256) void wy_kernel(WyArgs a) {
-  constexpr int C = kChunk;
-  constexpr int KP = K + 4;   // fp32 row pitch of gk_s
-  constexpr int KB = K + 8;   // bf16 row pitch of k_s / q_s / b_s / W staging
-  constexpr int CB = C + 8;   // row pitch of the column-major xw_s / xu_s
-  constexpr int LP = C + 4;   // fp32 row pitch of L_s / A_s / Aqk_s
-  constexpr int GKS = (C * KP * 4 > V * CB * 2 ? C * KP * 4 : V * CB * 2) / 4;
-  static_assert(C * KB * 2 <= K * CB * 2 + 1024, "W staging must fit in xw_s");
+// Row-wise selection of 4 consecutive entries x[4 q + e] with q = lane group (0..3).
+__device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
+  f32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = q == 0 ? x[e] : q == 1 ? x[4 + e] : q == 2 ? x[8 + e] : x[12 + e];
+  return r;
+}
 
-  __shared__ __attribute__((aligned(16))) float gk_s[GKS];  // later: xu_s (f16 [V][CB])
-  __shared__ __attribute__((aligned(16))) __bf16 k_s[C * KB];
-  __shared__ __attribute__((aligned(16))) __bf16 q_s[CAUSAL ? C * KB : 8];
-  __shared__ __attribute__((aligned(16))) __bf16 b_s[HAS_B ? C * KB : 8];
-  __shared__ __attribute__((aligned(16))) __bf16 xw_s[K * CB + 512];  // later: W staging [C][KB]
-  __shared__ __attribute__((aligned(16))) float L_s[C * LP];
-  __shared__ __attribute__((aligned(16))) float A_s[C * LP];
-  __shared__ __attribute__((aligned(16))) float Aqk_s[CAUSAL ? C * LP : 4];
-  __shared__ float tot_s[4 * K];
+template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT>
+__global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
+  constexpr int C = kChunk;
+  constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;
+  constexpr int XP = C + 8;   // element pitch of the column-major xw / xu tiles
+  constexpr int AP = C + 4;   // fp32 pitch of As_s
+  constexpr int LQ = 16 + 4;  // fp32 pitch of a diagonal L tile
+  constexpr int KBX = 6 * KS * 64 * 8;  // fp16 elements of the six off-diagonal operands
+  constexpr int XCH = KBX > K * XP ? KBX : K * XP;
+  constexpr float kWide = 96.f;  // in-block decay span (log2) beyond which exact products are used
+
+  __shared__ __attribute__((aligned(16))) float tot_s[4 * K];    // block sums of g
+  __shared__ __attribute__((aligned(16))) float first_s[4 * K];  // g (or gk) of each block's first token
+  __shared__ __attribute__((aligned(16))) float last_s[K];       // gk of the last valid token (G_CUM)
+  // per channel: rows 0-3 gk at the block starts, 4-6 2^(start_{w+1} - start_w),
+  // 7-10 2^(gk_last - start_w), 11-14 2^start_w, 15 gk_last
+  __shared__ __attribute__((aligned(16))) float fac_s[16 * K];
+  __shared__ __attribute__((aligned(16))) _Float16 xch_s[XCH];   // off-diagonal operands, then xw (bf16)
+  __shared__ __attribute__((aligned(16))) _Float16 xu_s[V * XP];  // column-major beta v
+  __shared__ __attribute__((aligned(16))) float As_s[C * AP];     // A, row-major
+  __shared__ __attribute__((aligned(16))) float Ld_s[4 * 16 * LQ];
+  __bf16* const xw_s = (__bf16*)xch_s;
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int tok0 = a.chunk_tok0[chunk];
-  const int len = a.chunk_len[chunk];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int tok0 = a.chunk_tok0[chunk], len = a.chunk_len[chunk];
   const size_t unit = (size_t)chunk * H + h;
+  const int t = 16 * wave + lr;
+  const bool valid = t < len;
+  const size_t rowK = ((size_t)(tok0 + (valid ? t : 0)) * H + h) * K;
+  const size_t rowV = ((size_t)(tok0 + (valid ? t : 0)) * H + h) * V;
 
-  // ---- phase 1: issue every global load of the chunk at once (k, q, b, g and
-  //      the v / beta operands of phase 4), stage k / q / b, decay cumsum ----
-  constexpr int K8 = K / 8;
-  constexpr int V8 = V / 8;
-  constexpr int NKL = C * K8 / 256;  // 16-byte k/q/b loads per thread
-  constexpr int NVL = C * V8 / 256;  // 8-element v/beta groups per thread
-  static_assert(NKL * 256 == C * K8 && NVL * 256 == C * V8, "load tiling");
-  constexpr int TPC = (256 / K) < 1 ? 1 : (256 / K);  // threads per channel
-  constexpr int SEG = C / TPC;
-  u32x4 kv[NKL], qv[CAUSAL ? NKL : 1], bv[HAS_B ? NKL : 1];
+  // ---- loads: every per-token input of this lane's row, in slot order ----
+  bf16x8 kraw[KS], braw[HAS_B ? KS : 1], qraw[CAUSAL ? KS : 1];
+  float g[KS][8];
+  f16x8 xu8[VS];
 #pragma unroll
-  for (int i = 0; i < NKL; ++i) {
-    const int idx = tid + 256 * i;
-    const int t = idx / K8, c8 = (idx % K8) * 8;
-    const size_t goff = ((size_t)(tok0 + t) * H + h) * K + c8;
-    kv[i] = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (CAUSAL) qv[i] = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (HAS_B) bv[i] = u32x4{0u, 0u, 0u, 0u};
-    if (t < len) {
-      kv[i] = *(const u32x4*)(a.k + goff);
-      if constexpr (CAUSAL) qv[i] = *(const u32x4*)(a.q + goff);
-      if constexpr (HAS_B) bv[i] = *(const u32x4*)(a.b + goff);
-    }
-  }
-  float gv[SEG];
-  {
-    const int c = tid % K, seg = tid / K;
+  for (int s = 0; s < KS; ++s) {
 #pragma unroll
-    for (int i = 0; i < SEG; ++i) {
-      const int t = seg * SEG + i;
-      gv[i] = (tid < K * TPC && t < len) ? a.g[((size_t)(tok0 + t) * H + h) * K + c] : 0.f;
-    }
-  }
-  bf16x8 vreg[NVL];
-  float breg[NVL][8];
-#pragma unroll
-  for (int i = 0; i < NVL; ++i) {
-    const int idx = tid + 256 * i;
-    const int t = idx / V8, c8 = (idx % V8) * 8;
-    const size_t goff = ((size_t)(tok0 + t) * H + h) * V + c8;
-    if (t < len) {
-      vreg[i] = *(const bf16x8*)(a.v + goff);
-      if constexpr (sizeof(BetaT) == 4) {
-        const f32x4 b0 = *(const f32x4*)((const float*)a.beta + goff);
-        const f32x4 b1 = *(const f32x4*)((const float*)a.beta + goff + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          breg[i][e] = b0[e];
-          breg[i][4 + e] = b1[e];
-        }
-      } else {
-        const bf16x8 bb = *(const bf16x8*)((const __bf16*)a.beta + goff);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) breg[i][e] = (float)bb[e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vreg[i][e] = (__bf16)0.f;
-        breg[i][e] = 0.f;
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < NKL; ++i) {
-    const int idx = tid + 256 * i;
-    const int t = idx / K8, c8 = (idx % K8) * 8;
-    *(u32x4*)(&k_s[t * KB + c8]) = kv[i];
-    if constexpr (CAUSAL) *(u32x4*)(&q_s[t * KB + c8]) = qv[i];
-    if constexpr (HAS_B) *(u32x4*)(&b_s[t * KB + c8]) = bv[i];
-  }
-  for (int idx = tid; idx < C * LP; idx += 256) A_s[idx] = 0.f;
-
-  if (tid < K * TPC) {
-    const int c = tid % K, seg = tid / K;
-    float run = 0.f;
-#pragma unroll
-    for (int i = 0; i < SEG; ++i) {
-      const int t = seg * SEG + i;
-      if constexpr (G_CUM) {
-        gk_s[t * KP + c] = gv[i];
-      } else {
-        run += gv[i];
-        gk_s[t * KP + c] = run;
-      }
-    }
-    if constexpr (!G_CUM) tot_s[seg * K + c] = run;
-  }
-  __syncthreads();
-  if (tid < K * TPC) {
-    const int c = tid % K, seg = tid / K;
-    if constexpr (!G_CUM) {
-      float off = 0.f;
-      for (int s2 = 0; s2 < seg; ++s2) off += tot_s[s2 * K + c];
-#pragma unroll
-      for (int i = 0; i < SEG; ++i) {
-        const int t = seg * SEG + i;
-        gk_s[t * KP + c] = (gk_s[t * KP + c] + off) * kRcpLn2;
-      }
-    } else {
-      // padding rows repeat the last valid cumulative decay
-      const float last = gk_s[(len - 1) * KP + c];
-#pragma unroll
-      for (int i = 0; i < SEG; ++i) {
-        const int t = seg * SEG + i;
-        if (t >= len) gk_s[t * KP + c] = last;
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 2: L (and scale * Aqk) row block I = wave ----------------------
-  {
-    const int I = wave, n = 16 * I;
-    const int r = n + (lane & 15);
-    // Largest in-block decay exponent; bounded factors keep fp32 exact.
-    float emax = 0.f;
-    for (int c = lane; c < K; c += 64) {
-      const float gn = gk_s[n * KP + c];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) emax = fmaxf(emax, gn - gk_s[(n + j) * KP + c]);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) emax = fmaxf(emax, __shfl_xor(emax, off, 64));
-
-    if (emax <= 64.f) {
-      f32x4 accL = zero4(), accQ = zero4();
-#pragma unroll 4
-      for (int s = 0; s < K / 4; ++s) {
-        const int c = 4 * s + (lane >> 4);
-        const float gr = gk_s[r * KP + c], gn = gk_s[n * KP + c];
-        const float kr = (float)k_s[r * KB + c];
-        const float bk = HAS_B ? kr * (float)b_s[r * KB + c] : kr;
-        const float fa = fast_exp2(gr - gn);  // <= 1
-        const float fb = fast_exp2(gn - gr);  // >= 1, <= 2^64
-        accL = mfma_f32(bk * fa, kr * fb, accL);
-        if constexpr (CAUSAL) accQ = mfma_f32((float)q_s[r * KB + c] * fa, kr * fb, accQ);
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      bf16x4 kk{}, bb{}, qq{};
+      f32x4 gg = zero4();
+      if (valid) {
+        kk = *(const bf16x4*)(a.k + rowK + c0);
+        if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
+        if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
+        gg = *(const f32x4*)(a.g + rowK + c0);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = 4 * (lane >> 4) + e, j = lane & 15;
-        L_s[(n + i) * LP + n + j] = (j < i) ? accL[e] : 0.f;
-        if constexpr (CAUSAL) Aqk_s[(n + i) * LP + n + j] = (j <= i) ? a.scale * accQ[e] : 0.f;
+        kraw[s][4 * half + e] = kk[e];
+        if constexpr (HAS_B) braw[s][4 * half + e] = bb[e];
+        if constexpr (CAUSAL) qraw[s][4 * half + e] = qq[e];
+        g[s][4 * half + e] = gg[e];
       }
+    }
+  }
+  auto kf = [&](int s, int j) { return (float)kraw[s][j]; };
+  auto bkf = [&](int s, int j) { return HAS_B ? (float)kraw[s][j] * (float)braw[s][j] : (float)kraw[s][j]; };
+  auto qf = [&](int s, int j) { return CAUSAL ? (float)qraw[s][j] : 0.f; };
+#pragma unroll
+  for (int s = 0; s < VS; ++s) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      bf16x4 vv{};
+      f32x4 bt = zero4();
+      if (valid) {
+        vv = *(const bf16x4*)(a.v + rowV + c0);
+        if constexpr (sizeof(BetaT) == 4) {
+          bt = *(const f32x4*)((const float*)a.beta + rowV + c0);
+        } else {
+          const bf16x4 b4 = *(const bf16x4*)((const __bf16*)a.beta + rowV + c0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bt[e] = (float)b4[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xu8[s][4 * half + e] = (_Float16)((float)vv[e] * bt[e]);
+    }
+  }
+
+  // Identity-matrix selectors: element j of lane (lr, lg) is 1 where the slot's channel
+  // is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
+  // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
+  f16x8 sel_h[2];
+  bf16x8 sel_b[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool one = (j >> 2) == half && 4 * lg + (j & 3) == lr;
+      sel_h[half][j] = (_Float16)(one ? 1.f : 0.f);
+      sel_b[half][j] = (__bf16)(one ? 1.f : 0.f);
+    }
+  // beta v to LDS now, column-major (channel rows, token columns)
+#pragma unroll
+  for (int ct = 0; ct < VT; ++ct) {
+    const f32x4 tr = mfma_f16(xu8[ct >> 1], sel_h[ct & 1], zero4());
+    f16x4 o4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
+    *(f16x4*)(&xu_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
+  }
+
+  // ---- cumsum: inclusive within the 16-token block, then block offsets ----
+  float gk[KS][8];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gk[s][j] = G_CUM ? g[s][j] : row_inclusive_scan(g[s][j]);
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const f32x4 gkv{gk[s][4 * half], gk[s][4 * half + 1], gk[s][4 * half + 2], gk[s][4 * half + 3]};
+      const f32x4 gv{g[s][4 * half], g[s][4 * half + 1], g[s][4 * half + 2], g[s][4 * half + 3]};
+      if (!G_CUM && lr == 15) *(f32x4*)(&tot_s[wave * K + c0]) = gkv;
+      if (lr == 0) *(f32x4*)(&first_s[wave * K + c0]) = gv;
+      if (G_CUM && t == len - 1) *(f32x4*)(&last_s[c0]) = gv;
+    }
+  lds_barrier();
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      if constexpr (!G_CUM) {
+        f32x4 base = zero4();
+        for (int w2 = 0; w2 < wave; ++w2) base += *(const f32x4*)(&tot_s[w2 * K + c0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gk[s][4 * half + e] = (base[e] + gk[s][4 * half + e]) * kRcpLn2;
+      } else if (!valid) {
+        const f32x4 lv = *(const f32x4*)(&last_s[c0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gk[s][4 * half + e] = lv[e];
+      }
+    }
+  if (tid < K) {
+    const int c = tid;
+    float ref[4], last;
+    if constexpr (!G_CUM) {
+      // same summation order as the per-lane offsets above, so fa == 1 exactly at block starts
+      float run = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        ref[w2] = (run + first_s[w2 * K + c]) * kRcpLn2;
+        run += tot_s[w2 * K + c];
+      }
+      last = run * kRcpLn2;
     } else {
-      // exact pairwise products, 2^(gk_i - gk_j) with j <= i only
-      for (int p = lane; p < 256; p += 64) {
-        const int i = p >> 4, j = p & 15;
-        float sl = 0.f, sq = 0.f;
-        if (j <= i) {
-          for (int c = 0; c < K; ++c) {
-            const float f = fast_exp2(gk_s[(n + i) * KP + c] - gk_s[(n + j) * KP + c]);
-            const float kj = (float)k_s[(n + j) * KB + c];
-            const float ki = (float)k_s[(n + i) * KB + c];
-            const float bki = HAS_B ? ki * (float)b_s[(n + i) * KB + c] : ki;
-            sl += bki * kj * f;
-            if constexpr (CAUSAL) sq += (float)q_s[(n + i) * KB + c] * kj * f;
-          }
-        }
-        L_s[(n + i) * LP + n + j] = (j < i) ? sl : 0.f;
-        if constexpr (CAUSAL) Aqk_s[(n + i) * LP + n + j] = (j <= i) ? a.scale * sq : 0.f;
-      }
+      last = last_s[c];
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) ref[w2] = (16 * w2 < len) ? first_s[w2 * K + c] : last;
     }
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) {
+      fac_s[w2 * K + c] = ref[w2];
+      if (w2 < 3) fac_s[(4 + w2) * K + c] = fast_exp2(ref[w2 + 1] - ref[w2]);
+      fac_s[(7 + w2) * K + c] = fast_exp2(last - ref[w2]);
+      fac_s[(11 + w2) * K + c] = fast_exp2(ref[w2]);
+    }
+    fac_s[15 * K + c] = last;
+    a.out.decay[unit * K + c] = fast_exp2(last);
+  }
+  lds_barrier();
 
-    // off-diagonal blocks J < I, re-centred at n: both factors <= 1 (fp16 safe)
-    if (I > 0) {
-      f16x8 aop[K / 32];
-      f16x8 qop[CAUSAL ? K / 32 : 1];
+  // ---- in-block decay span: a wide block takes exact diagonal products ----
+  float span = 0.f;
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
+  for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int c = 32 * s + 8 * (lane >> 4) + e;
-          const float fa = fast_exp2(gk_s[r * KP + c] - gk_s[n * KP + c]);
-          const float kr = (float)k_s[r * KB + c];
-          const float bk = HAS_B ? kr * (float)b_s[r * KB + c] : kr;
-          aop[s][e] = (_Float16)(bk * fa);
-          if constexpr (CAUSAL) qop[s][e] = (_Float16)((float)q_s[r * KB + c] * fa);
+    for (int half = 0; half < 2; ++half) {
+      const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + 32 * s + 16 * half + 4 * lg]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) span = fmaxf(span, r4[e] - gk[s][4 * half + e]);
+    }
+  const bool wide = __builtin_amdgcn_readfirstlane(wave_max(span) > kWide ? 1 : 0) != 0;
+  f32x4 Ld4 = zero4(), Qd4 = zero4();  // diagonal L / Aqk tiles (row lr, cols 4 lg + e)
+  if (wide) {
+    // lane (lr, lg) sums its own channels for the columns j of the block, reading the
+    // column tokens through shuffles inside its lane group; the four groups then add up
+    float pl[16], pq[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) pl[j] = pq[j] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float gj = __shfl(gk[s][jj], j + 16 * lg, 64);
+          const float kj = __shfl(kf(s, jj), j + 16 * lg, 64);
+          const float f = j <= lr ? fast_exp2(gk[s][jj] - gj) : 0.f;
+          pl[j] += bkf(s, jj) * kj * f;
+          if constexpr (CAUSAL) pq[j] += qf(s, jj) * kj * f;
         }
       }
-      for (int J = 0; J < I; ++J) {
-        const int jr = 16 * J + (lane & 15);
-        f32x4 aL = zero4(), aQ = zero4();
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s) {
-          f16x8 bop;
+    for (int j = 0; j < 16; ++j) {
+      pl[j] += __shfl_xor(pl[j], 16, 64);
+      pl[j] += __shfl_xor(pl[j], 32, 64);
+      if constexpr (CAUSAL) {
+        pq[j] += __shfl_xor(pq[j], 16, 64);
+        pq[j] += __shfl_xor(pq[j], 32, 64);
+      }
+    }
+    Ld4 = pick4(pl, lg);
+    Qd4 = pick4(pq, lg);
+  }
+
+  // ---- per channel step: factors, operands, the diagonal tiles and the outputs ----
+  // Off-diagonal column operands are built by wave J for row blocks I > J:
+  // k 2^(start_I - gk) = k (1/fa) prod_{w=J}^{I-1} 2^(start_{w+1} - start_w), each factor <= 1.
+  auto pair_index = [](int I, int J) { return J * (7 - J) / 2 + (I - J - 1); };
+  f16x8 a16[KS], aq16[CAUSAL ? KS : 1];
+  bf16x8 xw8[KS];
+  _Float16* const kg_out = a.out.kgT + unit * (size_t)(C * K);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int c = 32 * s + 8 * (lane >> 4) + e;
-            bop[e] = (_Float16)((float)k_s[jr * KB + c] * fast_exp2(gk_s[n * KP + c] - gk_s[jr * KP + c]));
-          }
-          aL = mfma_f16(aop[s], bop, aL);
-          if constexpr (CAUSAL) aQ = mfma_f16(qop[s], bop, aQ);
-        }
+  for (int s = 0; s < KS; ++s) {
+    bf16x8 ahi, alo, khi, klo, qhi, qlo, qg8;
+    f16x8 kg8;
+    float base[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = n + 4 * (lane >> 4) + e, j = 16 * J + (lane & 15);
-          L_s[i * LP + j] = aL[e];
-          if constexpr (CAUSAL) Aqk_s[i * LP + j] = a.scale * aQ[e];
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + c0]);
+      const f32x4 gw = *(const f32x4*)(&fac_s[(7 + wave) * K + c0]);
+      const f32x4 ew = *(const f32x4*)(&fac_s[(11 + wave) * K + c0]);
+      const f32x4 lastv = *(const f32x4*)(&fac_s[15 * K + c0]);
+      const int wn = wave < 3 ? wave : 2;
+      const f32x4 dj = *(const f32x4*)(&fac_s[(4 + wn) * K + c0]);
+      const f32x4 rn = *(const f32x4*)(&fac_s[(wn + 1) * K + c0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = 4 * half + e;
+        const float d = gk[s][j] - r4[e];  // <= 0
+        const float fa = fast_exp2(d), ifa = fast_exp2(-d);
+        const float av = bkf(s, j) * fa;
+        ahi[j] = (__bf16)av;
+        alo[j] = (__bf16)(av - (float)ahi[j]);
+        a16[s][j] = (_Float16)av;
+        xw8[s][j] = (__bf16)(av * ew[e]);
+        const float kbv = kf(s, j) * ifa;
+        khi[j] = (__bf16)kbv;
+        klo[j] = (__bf16)(kbv - (float)khi[j]);
+        kg8[j] = (_Float16)(wide ? kf(s, j) * fast_exp2(lastv[e] - gk[s][j]) : kbv * gw[e]);
+        base[j] = kf(s, j) * (wide ? fast_exp2(rn[e] - gk[s][j]) : ifa * dj[e]);
+        if constexpr (CAUSAL) {
+          const float qv = qf(s, j) * fa;
+          qhi[j] = (__bf16)qv;
+          qlo[j] = (__bf16)(qv - (float)qhi[j]);
+          aq16[s][j] = (_Float16)qv;
+          qg8[j] = (__bf16)(qv * ew[e]);
         }
       }
     }
-    // blocks above the diagonal
-    for (int idx = lane; idx < 16 * C; idx += 64) {
-      const int i = n + idx / C, j = idx % C;
-      if (j >= n + 16) {
-        L_s[i * LP + j] = 0.f;
-        if constexpr (CAUSAL) Aqk_s[i * LP + j] = 0.f;
+    if (!wide) {
+      Ld4 = mfma_bf16(khi, ahi, Ld4);
+      Ld4 = mfma_bf16(khi, alo, Ld4);
+      Ld4 = mfma_bf16(klo, ahi, Ld4);
+      if constexpr (CAUSAL) {
+        Qd4 = mfma_bf16(khi, qhi, Qd4);
+        Qd4 = mfma_bf16(khi, qlo, Qd4);
+        Qd4 = mfma_bf16(klo, qhi, Qd4);
+      }
+    }
+    if constexpr (CAUSAL)
+      *(bf16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + s) * 64 + lane) * 8) = qg8;
+    // kg^T to global as P-frags (rows = channels, reduction = tokens)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int ct = 2 * s + half;
+      const f32x4 tr = mfma_f16(kg8, sel_h[half], zero4());
+      f16x4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
+      *(f16x4*)(kg_out + ((size_t)(ct * 2 + (wave >> 1)) * 64 + lane) * 8 + (wave & 1) * 4) = o4;
+    }
+    if (wave < 3) {
+#pragma unroll
+      for (int I = 1; I < 4; ++I) {
+        if (I <= wave) continue;
+        if (I > wave + 1) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const f32x4 dn = *(const f32x4*)(&fac_s[(4 + I - 1) * K + 32 * s + 16 * half + 4 * lg]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) base[4 * half + e] *= dn[e];
+          }
+        }
+        f16x8 op;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) op[j] = (_Float16)base[j];
+        *(f16x8*)(&xch_s[((size_t)(pair_index(I, wave) * KS + s) * 64 + lane) * 8]) = op;
       }
     }
   }
-  __syncthreads();
+  lds_barrier();  // off-diagonal operands visible
 
-  // ---- phase 3: diagonal inverses (wave 0) and the elementwise operands -----
-  if (wave == 0) {
-    const int I = lane >> 4, j = lane & 15, n = 16 * I;
-    float x[16];
+  // ---- L and Aqk tiles (I = wave, J <= I), transposed: lane holds row lr, cols 4 lg + e ----
+  f32x4 Lt[4], Qt[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float sum = (i == j) ? 1.f : 0.f;
-#pragma unroll
-      for (int m = 0; m < i; ++m) sum -= L_s[(n + i) * LP + n + m] * x[m];
-      x[i] = sum;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) A_s[(n + i) * LP + n + j] = x[i];
+  for (int J = 0; J < 4; ++J) {
+    Lt[J] = J == wave ? Ld4 : zero4();
+    Qt[J] = J == wave ? Qd4 : zero4();
   }
+#pragma unroll
+  for (int J = 0; J < 3; ++J) {
+    if (J >= wave) continue;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const f16x8 op = *(const f16x8*)(&xch_s[((size_t)(pair_index(wave, J) * KS + s) * 64 + lane) * 8]);
+      Lt[J] = mfma_f16(op, a16[s], Lt[J]);
+      if constexpr (CAUSAL) Qt[J] = mfma_f16(op, aq16[s], Qt[J]);
+    }
+  }
+  // masks: L strictly lower, Aqk lower with the diagonal, scaled
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int col = 4 * lg + e;
+      const bool diag = J == wave;
+      if (J > wave || (diag && col >= lr)) Lt[J][e] = 0.f;
+      if constexpr (CAUSAL) Qt[J][e] = (J > wave || (diag && col > lr)) ? 0.f : a.scale * Qt[J][e];
+    }
+  }
+  if constexpr (CAUSAL) {
+    _Float16* aq_out = a.out.Aqk + unit * (size_t)(C * C);
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      f16x4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (_Float16)Qt[J][e];
+      *(f16x4*)(aq_out + ((size_t)(wave * 2 + (J >> 1)) * 64 + lane) * 8 + (J & 1) * 4) = o4;
+    }
+  }
+
+  // ---- A_II by row substitution: x (I + L_II) = e_lr, x[m] = d_lm - sum_{p>m} x[p] L[p][m] ----
+  f32x4 Aii;
   {
-    // kg^T P-frag (rows = K channel, red = tokens) to global, xw (col-major) to LDS.
-    _Float16* kg_out = a.out.kgT + unit * (size_t)(C * K);
-    for (int grp = tid; grp < K * C / 8; grp += 256) {
-      const int lane_f = grp & 63, rs = grp >> 6;  // rs = rt * 2 + s
-      const int s = rs & 1, rt = rs >> 1;
-      const int m = 16 * rt + (lane_f & 15);
-      const float glast = gk_s[(C - 1) * KP + m];
-      f16x8 kgv;
+    float* Ld = Ld_s + wave * 16 * LQ;
+    f32x4 ld4 = zero4();
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int t0 = 32 * s + 16 * half + 4 * (lane_f >> 4);
-        bf16x4 xwv;
+    for (int J = 0; J < 4; ++J)
+      if (J == wave) ld4 = Lt[J];
+    *(f32x4*)(&Ld[lr * LQ + 4 * lg]) = ld4;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's own tile is in LDS
+    __builtin_amdgcn_wave_barrier();
+    float x[16], acc[16];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = t0 + e;
-          const float gt = gk_s[t * KP + m];
-          const float kt = (float)k_s[t * KB + m];
-          const float bk = HAS_B ? kt * (float)b_s[t * KB + m] : kt;
-          kgv[4 * half + e] = (_Float16)(kt * fast_exp2(glast - gt));
-          xwv[e] = (__bf16)(bk * fast_exp2(gt));
-        }
-        *(bf16x4*)(&xw_s[m * CB + t0]) = xwv;
-      }
-      *(f16x8*)(kg_out + (size_t)grp * 8) = kgv;
-    }
-    for (int c = tid; c < K; c += 256) a.out.decay[unit * K + c] = fast_exp2(gk_s[(C - 1) * KP + c]);
-    if constexpr (CAUSAL) {
-      __bf16* qg_out = a.out.qg + unit * (size_t)(C * K);
-      for (int grp = tid; grp < C * K / 8; grp += 256) {
-        const int lane_f = grp & 63, rs = grp >> 6;  // rs = rt * (K/32) + s
-        const int s = rs % (K / 32), rt = rs / (K / 32);
-        const int t = 16 * rt + (lane_f & 15);
-        bf16x8 qv;
+    for (int m = 0; m < 16; ++m) acc[m] = 0.f;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int c0 = 32 * s + 16 * half + 4 * (lane_f >> 4);
+    for (int p = 15; p >= 0; --p) {
+      x[p] = (p == lr ? 1.f : 0.f) - acc[p];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            qv[4 * half + e] = (__bf16)((float)q_s[t * KB + c0 + e] * fast_exp2(gk_s[t * KP + c0 + e]));
-        }
-        *(bf16x8*)(qg_out + (size_t)grp * 8) = qv;
+      for (int q4 = 0; q4 < 4; ++q4) {
+        if (4 * q4 >= p) continue;
+        const f32x4 row = *(const f32x4*)(&Ld[p * LQ + 4 * q4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (4 * q4 + e < p) acc[4 * q4 + e] += x[p] * row[e];
       }
     }
+    Aii = pick4(x, lg);
   }
-  __syncthreads();
+  *(f32x4*)(&As_s[(16 * wave + lr) * AP + 16 * wave + 4 * lg]) = Aii;
+#pragma unroll
+  for (int J = 0; J < 4; ++J)
+    if (J > wave) *(f32x4*)(&As_s[(16 * wave + lr) * AP + 16 * J + 4 * lg]) = zero4();
+  lds_barrier();  // A_II visible; the off-diagonal operands are dead
 
-  // ---- phase 4: xu = beta * v (f16, column-major, aliases gk_s) and the
-  //      off-diagonal inverse blocks -----------------------------------------
-  _Float16* xu_s = (_Float16*)gk_s;
+  // xw, column-major (channel rows, token columns), by identity transposes
 #pragma unroll
-  for (int i = 0; i < NVL; ++i) {
-    const int idx = tid + 256 * i;
-    const int t = idx / V8, c8 = (idx % V8) * 8;
+  for (int ct = 0; ct < KT; ++ct) {
+    const f32x4 tr = mfma_bf16(xw8[ct >> 1], sel_b[ct & 1], zero4());
+    bf16x4 o4;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xu_s[(c8 + e) * CB + t] = (_Float16)((float)vreg[i][e] * breg[i][e]);
+    for (int e = 0; e < 4; ++e) o4[e] = (__bf16)tr[e];
+    *(bf16x4*)(&xw_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
   }
-  // A_{I+d, I} for d = 1, 2, 3 (one 16x16 block per wave per stage).
+
+  // ---- A_IJ = -A_II sum_{M=J}^{I-1} L_IM A_MJ, stage d = I - J ----
 #pragma unroll
   for (int d = 1; d <= 3; ++d) {
-    if (wave < 4 - d) {
-      const int J = wave, I = wave + d;
-      // T = sum_{M=J}^{I-1} L_IM A_MJ   (standard K order)
+    if (wave >= d) {
+      const int J = wave - d;
       f32x4 T = zero4();
-      for (int M = J; M < I; ++M) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int kk = 4 * s + (lane >> 4);
-          const float av = L_s[(16 * I + (lane & 15)) * LP + 16 * M + kk];
-          const float bv = A_s[(16 * M + kk) * LP + 16 * J + (lane & 15)];
-          T = mfma_f32(av, bv, T);
+      for (int M = 0; M < 3; ++M) {
+        if (M < J || M >= wave) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float bv = As_s[(16 * M + 4 * lg + e) * AP + 16 * J + lr];
+          T = mfma_f32(Lt[M][e], bv, T);
         }
       }
-      // R = A_II T, contracting index k = 4*(lane/16) + s so T's C layout is the B operand.
       f32x4 R = zero4();
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float av = A_s[(16 * I + (lane & 15)) * LP + 16 * I + 4 * (lane >> 4) + s];
-        R = mfma_f32(av, T[s], R);
-      }
+      for (int e = 0; e < 4; ++e) R = mfma_f32(Aii[e], T[e], R);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        A_s[(16 * I + 4 * (lane >> 4) + e) * LP + 16 * J + (lane & 15)] = -R[e];
+      for (int e = 0; e < 4; ++e) As_s[(16 * wave + 4 * lg + e) * AP + 16 * J + lr] = -R[e];
     }
-    __syncthreads();
+    lds_barrier();
   }
 
-  // ---- phase 5: W = A xw (bf16), U = A xu (f16), row tile R = wave ----------
+  // ---- W^T = xw^T A^T (bf16) and U = A xu (fp16), row block R = wave ----
   {
     const int R = wave;
-    bf16x8 ab[2];
-    f16x8 ah[2];
+    constexpr int NS = 2;  // 32-token reduction steps
+    bf16x8 ab[NS];
+    f16x8 ah[NS];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < NS; ++s) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float av = A_s[(16 * R + (lane & 15)) * LP + 32 * s + 8 * (lane >> 4) + e];
-        ab[s][e] = (__bf16)av;
-        ah[s][e] = (_Float16)av;
+      for (int half = 0; half < 2; ++half) {
+        const f32x4 r4 = *(const f32x4*)(&As_s[(16 * R + lr) * AP + 32 * s + 16 * half + 4 * lg]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ab[s][4 * half + e] = (__bf16)r4[e];
+          ah[s][4 * half + e] = (_Float16)r4[e];
+        }
       }
     }
-    // U tiles straight to global in C-frag order
-    _Float16* U_out = a.out.U + unit * (size_t)(C * V);
+    const bool two = R >= 2;  // row blocks 0, 1 have no entries past token 31
+    __bf16* W_out = a.out.W + unit * (size_t)(C * K);
 #pragma unroll
-    for (int ct = 0; ct < V / 16; ++ct) {
+    for (int ct = 0; ct < KT; ++ct) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const f16x8 bv = *(const f16x8*)(&xu_s[(16 * ct + (lane & 15)) * CB + 32 * s + 8 * (lane >> 4)]);
-        acc = mfma_f16(ah[s], bv, acc);
+      for (int s = 0; s < NS; ++s) {
+        if (s == 1 && !two) continue;
+        const __bf16* col = xw_s + (16 * ct + lr) * XP + 32 * s + 4 * lg;
+        const bf16x4 lo = *(const bf16x4*)col;
+        const bf16x4 hi = *(const bf16x4*)(col + 16);
+        const bf16x8 xa{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc = mfma_bf16(xa, ab[s], acc);
+      }
+      bf16x4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (__bf16)acc[e];
+      *(bf16x4*)(W_out + ((size_t)(R * KS + (ct >> 1)) * 64 + lane) * 8 + (ct & 1) * 4) = o4;
+    }
+    _Float16* U_out = a.out.U + unit * (size_t)(C * V);
+#pragma unroll
+    for (int ct = 0; ct < VT; ++ct) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (s == 1 && !two) continue;
+        const _Float16* col = xu_s + (16 * ct + lr) * XP + 32 * s + 4 * lg;
+        const f16x4 lo = *(const f16x4*)col;
+        const f16x4 hi = *(const f16x4*)(col + 16);
+        const f16x8 xb{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc = mfma_f16(ah[s], xb, acc);
       }
       f16x4 o4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o4[e] = (_Float16)acc[e];
-      *(f16x4*)(U_out + ((size_t)(R * (V / 16) + ct) * 64 + lane) * 4) = o4;
-    }
-    f32x4 wacc[K / 16];
-#pragma unroll
-    for (int ct = 0; ct < K / 16; ++ct) {
-      wacc[ct] = zero4();
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 bv = *(const bf16x8*)(&xw_s[(16 * ct + (lane & 15)) * CB + 32 * s + 8 * (lane >> 4)]);
-        wacc[ct] = mfma_bf16(ab[s], bv, wacc[ct]);
-      }
-    }
-    __syncthreads();  // xw_s fully consumed: reuse it as the W staging buffer
-    __bf16* Wst = xw_s;
-#pragma unroll
-    for (int ct = 0; ct < K / 16; ++ct) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        Wst[(16 * R + 4 * (lane >> 4) + e) * KB + 16 * ct + (lane & 15)] = (__bf16)wacc[ct][e];
+      *(f16x4*)(U_out + ((size_t)(R * VT + ct) * 64 + lane) * 4) = o4;
     }
   }
-  __syncthreads();
-  {
-    const __bf16* Wst = xw_s;
-    __bf16* W_out = a.out.W + unit * (size_t)(C * K);
-    for (int grp = tid; grp < C * K / 8; grp += 256) {
-      const int lane_f = grp & 63, rs = grp >> 6;
-      const int s = rs % (K / 32), rt = rs / (K / 32);
-      const int t = 16 * rt + (lane_f & 15);
-      const int c0 = 32 * s + 4 * (lane_f >> 4);
-      const bf16x4 lo = *(const bf16x4*)(&Wst[t * KB + c0]);
-      const bf16x4 hi = *(const bf16x4*)(&Wst[t * KB + c0 + 16]);
-      *(bf16x8*)(W_out + (size_t)grp * 8) = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
-    if constexpr (CAUSAL) {
-      _Float16* Aqk_out = a.out.Aqk + unit * (size_t)(C * C);
-      for (int grp = tid; grp < C * C / 8; grp += 256) {
-        const int lane_f = grp & 63, rs = grp >> 6;
-        const int s = rs & 1, rt = rs >> 1;
-        const int t = 16 * rt + (lane_f & 15);
-        const int j0 = 32 * s + 4 * (lane_f >> 4);
-        f16x8 av;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          av[e] = (_Float16)Aqk_s[t * LP + j0 + e];
-          av[4 + e] = (_Float16)Aqk_s[t * LP + j0 + 16 + e];
-        }
-        *(f16x8*)(Aqk_out + (size_t)grp * 8) = av;
-      }
-    }
-    if (a.A_ref != nullptr) {
-      for (int idx = tid; idx < len * C; idx += 256) {
-        const int t = idx / C, j = idx % C;
-        a.A_ref[((size_t)(tok0 + t) * H + h) * C + j] = (__bf16)A_s[t * LP + j];
-      }
+  if (a.A_ref != nullptr) {
+    for (int idx = tid; idx < len * C; idx += 256) {
+      const int tt = idx / C, j = idx % C;
+      a.A_ref[((size_t)(tok0 + tt) * H + h) * C + j] = (__bf16)As_s[tt * AP + j];
     }
   }
 }
