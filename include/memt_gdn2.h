@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 1
+#define MEMT_GDN2_ABI_VERSION 2
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -86,9 +86,11 @@ int memt_gdn2_chunk_local_cumsum(const void* g, int g_dtype, float* gk, const me
                                  int H, int S, float scale, int reverse, void* stream);
 
 /*
- * Bytes of device workspace memt_gdn2_chunk_update needs for this plan.
+ * Bytes of device workspace memt_gdn2_chunk_update (and memt_gdn2_fwd_h, with
+ * out_mode NONE) needs for a plan of n_chunk chunks over n_seq sequences.
+ * Long sequences get a two-level scan whose group states live here too.
  */
-size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int H, int K, int V, int out_mode);
+size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int K, int V, int out_mode);
 
 /*
  * The chunked GDN-2 memory update (stable gated delta rule) end to end:

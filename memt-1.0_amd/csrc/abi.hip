@@ -56,9 +56,10 @@ int memt_gdn2_chunk_local_cumsum(const void* g, int g_dtype, float* gk, const me
                                  H, S, scale, reverse != 0, (hipStream_t)stream));
 }
 
-size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int H, int K, int V, int out_mode) {
-  if (n_chunk < 0 || H <= 0 || K <= 0 || V <= 0) return 0;
-  return wy_layout(n_chunk, H, K, V, out_mode == MEMT_GDN2_OUT_CAUSAL).total;
+size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int K, int V, int out_mode) {
+  if (n_chunk < 0 || n_seq < 0 || H <= 0 || K <= 0 || V <= 0) return 0;
+  const size_t wy = wy_layout(n_chunk, H, K, V, out_mode == MEMT_GDN2_OUT_CAUSAL).total;
+  return group_layout(wy, n_chunk, n_seq, H, K, V, nullptr, nullptr);
 }
 
 int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta,
@@ -82,7 +83,8 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
   }
   const bool causal = out_mode == MEMT_GDN2_OUT_CAUSAL;
   const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, causal);
-  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
+  const size_t need = group_layout(lay.total, plan->n_chunk, plan->n_seq, H, K, V, nullptr, nullptr);
+  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u)))
     return MEMT_GDN2_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   const WyBuffers buf = wy_buffers(workspace, lay, causal);
@@ -121,7 +123,10 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
   sa.o = causal ? (__bf16*)o : nullptr;
   sa.H = H;
   sa.n_seq = plan->n_seq;
+  sa.n_chunk = plan->n_chunk;
   sa.scale = scale;
+  sa.group_L = scan_group_chunks(plan->n_chunk, plan->n_seq, H, V);
+  group_layout(lay.total, plan->n_chunk, plan->n_seq, H, K, V, &sa.grp, workspace);
   return status_of(launch_state(sa, K, V, causal, st));
 }
 
@@ -169,7 +174,8 @@ int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* g
     return MEMT_GDN2_EINVAL;
   if (snaps != nullptr && (plan->chunk_flags == nullptr || plan->chunk_block_ids == nullptr)) return MEMT_GDN2_EINVAL;
   const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, false);
-  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
+  const size_t need = group_layout(lay.total, plan->n_chunk, plan->n_seq, H, K, V, nullptr, nullptr);
+  if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u)))
     return MEMT_GDN2_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   const WyBuffers buf = wy_buffers(workspace, lay, false);
@@ -189,7 +195,10 @@ int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* g
   sa.o = nullptr;
   sa.H = H;
   sa.n_seq = plan->n_seq;
+  sa.n_chunk = plan->n_chunk;
   sa.scale = 1.f;
+  sa.group_L = scan_group_chunks(plan->n_chunk, plan->n_seq, H, V);
+  group_layout(lay.total, plan->n_chunk, plan->n_seq, H, K, V, &sa.grp, workspace);
   return status_of(launch_state(sa, K, V, false, st));
 }
 

@@ -48,18 +48,18 @@ __host__ __device__ __forceinline__ int cfrag_index(int row, int col, int n) {
 __host__ __device__ __forceinline__ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Per-(chunk, head) records of the WY stage, unit u = chunk * H + head.
-//   W     bf16 [64 x K]  P-frag (rows = tokens, red = K)       erase path
+//   W     f16  [64 x K]  P-frag (rows = tokens, red = K)       erase path
 //   kgT   f16  [K x 64]  P-frag of kg^T (rows = K, red = tokens) value path
 //   U     f16  [64 x V]  C-frag                                 value path
 //   decay f32  [K]       2^{gk_last}
-//   qg    bf16 [64 x K]  P-frag, q * 2^{gk}                     (causal output)
+//   qg    f16  [64 x K]  P-frag, q * 2^{gk}                     (causal output)
 //   Aqk   f16  [64 x 64] P-frag, scale * causal scores          (causal output)
 struct WyBuffers {
-  __bf16* W;
+  _Float16* W;
   _Float16* kgT;
   _Float16* U;
   float* decay;
-  __bf16* qg;
+  _Float16* qg;
   _Float16* Aqk;
 };
 
@@ -84,11 +84,11 @@ inline WyLayout wy_layout(int n_chunk, int H, int K, int V, bool causal) {
 inline WyBuffers wy_buffers(void* ws, const WyLayout& l, bool causal) {
   char* base = (char*)ws;
   WyBuffers b;
-  b.W = (__bf16*)(base + l.off_W);
+  b.W = (_Float16*)(base + l.off_W);
   b.kgT = (_Float16*)(base + l.off_kg);
   b.U = (_Float16*)(base + l.off_U);
   b.decay = (float*)(base + l.off_decay);
-  b.qg = causal ? (__bf16*)(base + l.off_qg) : nullptr;
+  b.qg = causal ? (_Float16*)(base + l.off_qg) : nullptr;
   b.Aqk = causal ? (_Float16*)(base + l.off_Aqk) : nullptr;
   return b;
 }
@@ -108,6 +108,60 @@ struct WyArgs {
   __bf16* A_ref;       // optional [T,H,64] bf16 inverse (reference layout)
 };
 
+// Two-level scan.  A sequence's chunks are split into groups of L chunks.
+//   phase 1  per group (in parallel): the transition P_g = prod_c (Diag(decay_c) - kg_c^T W_c)
+//            and the zero-start contribution Q_g, by running the scan on [I | 0]
+//   phase 2  per sequence (serial over its groups): S_{g+1} = P_g S_g + Q_g
+//   phase 3  per group (in parallel): the scan proper from S_g, with its outputs
+// The group table is built on the device from seq_chunk_offsets.
+struct GroupBuffers {
+  int32_t* seq_group_offsets;    // [n_seq + 1]
+  int32_t* group_chunk_offsets;  // [n_group_bound + 1]
+  int32_t* group_seq;            // [n_group_bound]
+  float* P;                      // [n_group_bound, H, K, K]
+  float* Q;                      // [n_group_bound, H, K, V]
+  float* S0;                     // [n_group_bound, H, K, V] state entering each group
+};
+
+// Chunks per group for the two-level scan (0 = plain per-sequence scan).
+// Groups are used when the plain scan would occupy few workgroups and the
+// sequences are long; L is the smallest power of two >= 4 that keeps the
+// phase-3 grid near 512 workgroups (two per CU on 256 CUs).
+inline int scan_group_chunks(int n_chunk, int n_seq, int H, int V) {
+  if (n_seq <= 0 || n_chunk <= 0) return 0;
+  const long slices = V / 32;
+  if ((long)n_seq * H * slices >= 512) return 0;
+  int L = 4;
+  while ((long)(n_chunk / L) * H * slices > 512 && L < (1 << 20)) L *= 2;
+  if (n_chunk / n_seq < 2 * L) return 0;
+  return L;
+}
+inline int group_bound(int n_chunk, int n_seq, int L) { return n_chunk / L + n_seq + 1; }
+
+inline size_t group_layout(size_t base, int n_chunk, int n_seq, int H, int K, int V, GroupBuffers* out,
+                           void* ws) {
+  const int L = scan_group_chunks(n_chunk, n_seq, H, V);
+  if (L == 0) return base;
+  const size_t nb = (size_t)group_bound(n_chunk, n_seq, L);
+  size_t o = align256(base);
+  const size_t off_sgo = o; o = align256(o + (size_t)(n_seq + 1) * 4);
+  const size_t off_gco = o; o = align256(o + (nb + 1) * 4);
+  const size_t off_gseq = o; o = align256(o + nb * 4);
+  const size_t off_P = o; o = align256(o + nb * H * K * K * 4);
+  const size_t off_Q = o; o = align256(o + nb * H * K * V * 4);
+  const size_t off_S0 = o; o = align256(o + nb * H * K * V * 4);
+  if (out != nullptr) {
+    char* b = (char*)ws;
+    out->seq_group_offsets = (int32_t*)(b + off_sgo);
+    out->group_chunk_offsets = (int32_t*)(b + off_gco);
+    out->group_seq = (int32_t*)(b + off_gseq);
+    out->P = (float*)(b + off_P);
+    out->Q = (float*)(b + off_Q);
+    out->S0 = (float*)(b + off_S0);
+  }
+  return o;
+}
+
 struct StateArgs {
   WyBuffers in;
   const int32_t* chunk_tok0;
@@ -121,7 +175,10 @@ struct StateArgs {
   __bf16* o;           // [T,H,V] (causal) or null
   int H;
   int n_seq;
+  int n_chunk;
   float scale;
+  int group_L;         // chunks per group, 0 = plain scan
+  GroupBuffers grp;    // valid when group_L > 0
 };
 
 // Launchers (return hipError_t of the launch).

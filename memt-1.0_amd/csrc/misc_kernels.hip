@@ -230,9 +230,9 @@ __global__ __launch_bounds__(256) void wy_export_kernel(WyBuffers in, const int3
   for (int idx = threadIdx.x; idx < len * K; idx += 256) {
     const int t = idx / K, c = idx % K;
     const size_t dst = ((size_t)(tok0 + t) * H + h) * K + c;
-    if (w) w[dst] = in.W[unit * C * K + pfrag_index(t, c, K)];
+    if (w) w[dst] = (__bf16)(float)in.W[unit * C * K + pfrag_index(t, c, K)];
     if (kg) kg[dst] = (__bf16)(float)in.kgT[unit * C * K + pfrag_index(c, t, C)];
-    if (qg && in.qg) qg[dst] = in.qg[unit * C * K + pfrag_index(t, c, K)];
+    if (qg && in.qg) qg[dst] = (__bf16)(float)in.qg[unit * C * K + pfrag_index(t, c, K)];
   }
   for (int idx = threadIdx.x; idx < len * V; idx += 256) {
     const int t = idx / V, c = idx % V;
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const _
     const int t = idx / K, c = idx % K;
     const size_t src = ((size_t)(tok0 + t) * H + h) * K + c;
     const bool ok = t < len;
-    out.W[unit * C * K + pfrag_index(t, c, K)] = ok ? w[src] : (__bf16)0.f;
+    out.W[unit * C * K + pfrag_index(t, c, K)] = (_Float16)(ok ? (float)w[src] : 0.f);
     out.kgT[unit * C * K + pfrag_index(c, t, C)] = (_Float16)(ok ? (float)kg[src] : 0.f);
   }
   for (int idx = threadIdx.x; idx < C * V; idx += 256) {

@@ -7,12 +7,13 @@
 // (models/qwen/ops/_triton/state.py:76-115):
 //
 //   snapshot S if the chunk starts a read block
-//   V_new = U - W . bf16(S)                        (bf16 MFMA, erase path)
-//   o     = scale * qg . bf16(S) + Aqk . V_new      (causal output, optional)
-//   S     = decay * S + kg^T . f16(V_new)           (f16 MFMA, value path, if committed)
+//   V_new = U - W . f16(S)                         (erase path)
+//   o     = scale * qg . f16(S) + Aqk . V_new       (causal output, optional)
+//   S     = decay * S + kg^T . f16(V_new)           (value path, if committed)
+// Every product is fp16 MFMA with fp32 accumulation; S stays fp32.
 //
 // Wave w owns S rows [w*K/4, (w+1)*K/4) and V_new / o token rows [16w, 16w+16),
-// so it reads only its quarter of each chunk record.  bf16(S) and f16(V_new)
+// so it reads only its quarter of each chunk record.  f16(S) and f16(V_new)
 // cross waves through two column-major LDS tiles, with two LDS-only barriers
 // per chunk.  The W / qg / kg^T / Aqk records are P-frags, whose reduction
 // index pairs with B operands gathered as two 8-byte LDS reads per lane.
@@ -21,6 +22,12 @@
 // fragments and its plan entries) is loaded into registers two chunks ahead;
 // the loop is unrolled by two so the two register buffers alternate without
 // copies, and the compiler's vmcnt waits stay exact.
+//
+// Long sequences use a two-level scan over groups of chunks (the recurrence is
+// linear in S): the same kernel first runs on [I | 0] per group to form the
+// group transition P_g and its zero-start contribution Q_g (modes 1 and 2),
+// combine_kernel then chains S_{g+1} = P_g S_g + Q_g per sequence (split-bf16
+// MFMA, ~2^-16 relative), and the scan proper runs per group from S_g.
 #include "gdn2_internal.h"
 
 namespace memt {
@@ -31,8 +38,8 @@ struct ScanFrag {
   static constexpr int KS = K / 32;
   static constexpr int RT = K / 64;   // 16-row S tiles per wave
   static constexpr int CT = BV / 16;  // 16-column tiles per workgroup
-  bf16x8 w[KS];
-  bf16x8 qg[CAUSAL ? KS : 1];
+  f16x8 w[KS];
+  f16x8 qg[CAUSAL ? KS : 1];
   f16x8 kg[RT][2];
   f16x8 aq[CAUSAL ? 2 : 1];
   f16x4 u[CT];
@@ -40,19 +47,24 @@ struct ScanFrag {
   int flags, block, tok0, len;
 };
 
-template <int K, int V, int BV, bool CAUSAL>
+// MODE 0: the scan (per sequence, or per group from its start state)
+// MODE 1: group transition P_g, columns of the K x K identity, no values
+// MODE 2: group contribution Q_g, value columns from a zero state
+template <int K, int V, int BV, bool CAUSAL, int MODE>
 __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   using F = ScanFrag<K, V, BV, CAUSAL>;
   constexpr int C = kChunk;
-  constexpr int NV = V / BV;
+  constexpr int NC = MODE == 1 ? K : V;  // state columns of this mode
+  constexpr int NV = NC / BV;
+  static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
   constexpr int KS = F::KS;
   constexpr int RT = F::RT;
   constexpr int CT = F::CT;
-  constexpr int SKP = K + 8;  // pitch of column-major bf16(S)
+  constexpr int SKP = K + 8;  // pitch of column-major f16(S)
   constexpr int VNP = C + 8;  // pitch of column-major f16(V_new)
   static_assert(RT >= 1 && CT >= 1, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) __bf16 S_lds[BV * SKP];
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[BV * SKP];
   __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[BV * VNP];
 
   // XCD-aware order: the NV slices of one (sequence, head) share an XCD (and its L2),
@@ -62,16 +74,35 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   if ((total & 7) == 0) bid = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
   const int vs = bid % NV;
   const int h = (bid / NV) % a.H;
-  const int n = bid / (NV * a.H);
+  const int unitg = bid / (NV * a.H);  // sequence, or group when grouped
   const int H = a.H;
-  const int v0 = vs * BV;
+  const int v0 = vs * BV;  // first state column (of P for MODE 1, of V otherwise)
+
+  int c_begin, c_end, seq = unitg;
+  bool first = true, last = true;
+  if (a.group_L == 0) {
+    c_begin = a.seq_chunk_offsets[seq];
+    c_end = a.seq_chunk_offsets[seq + 1];
+  } else {
+    if (unitg >= a.grp.seq_group_offsets[a.n_seq]) return;
+    seq = a.grp.group_seq[unitg];
+    c_begin = a.grp.group_chunk_offsets[unitg];
+    c_end = a.grp.group_chunk_offsets[unitg + 1];
+    first = unitg == a.grp.seq_group_offsets[seq];
+    last = unitg + 1 == a.grp.seq_group_offsets[seq + 1];
+    if (MODE != 0 && last) return;  // the last group's transition is never used
+  }
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
 
   // S tile rt of this wave: rows 16*(w*RT + rt) + 4*lg + e, column v0 + 16*ct + lr
   f32x4 S[RT][CT];
-  const size_t state_off = ((size_t)n * H + h) * K * V;
+  const float* h0p = nullptr;
+  if constexpr (MODE == 0) {
+    if (!first) h0p = a.grp.S0 + ((size_t)unitg * H + h) * K * V;
+    else if (a.h0 != nullptr) h0p = a.h0 + ((size_t)seq * H + h) * K * V;
+  }
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -79,7 +110,9 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * (w * RT + rt) + 4 * lg + e;
-        S[rt][ct][e] = a.h0 ? a.h0[state_off + (size_t)row * V + v0 + 16 * ct + lr] : 0.f;
+        const int col = v0 + 16 * ct + lr;
+        if constexpr (MODE == 1) S[rt][ct][e] = row == col ? 1.f : 0.f;
+        else S[rt][ct][e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
       }
   // settle the initial-state loads here: otherwise every later use of S in the
   // loop would wait for all outstanding loads, prefetches included
@@ -91,10 +124,10 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        bf16x4 b4;
+        f16x4 b4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) b4[e] = (__bf16)S[rt][ct][e];
-        *(bf16x4*)(&S_lds[(16 * ct + lr) * SKP + 16 * (w * RT + rt) + 4 * lg]) = b4;
+        for (int e = 0; e < 4; ++e) b4[e] = (_Float16)S[rt][ct][e];
+        *(f16x4*)(&S_lds[(16 * ct + lr) * SKP + 16 * (w * RT + rt) + 4 * lg]) = b4;
       }
   };
 
@@ -102,7 +135,6 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   // with readlane.  Loading them per chunk would make the compiler move each
   // entry to a scalar register right after its load, waiting for every
   // outstanding prefetch; this way the wait comes once per 64 chunks.
-  const int c_begin = a.seq_chunk_offsets[n], c_end = a.seq_chunk_offsets[n + 1];
   int mbase = c_begin - 64;
   int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0;
   auto meta = [&](int c, F& f) {
@@ -111,7 +143,7 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
       const int cc = c + lane;
       const bool ok = cc < c_end;
       m_flags = !ok ? 0 : a.chunk_flags ? a.chunk_flags[cc] : MEMT_GDN2_CHUNK_COMMIT;
-      m_block = (ok && a.snaps != nullptr && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
+      m_block = (MODE == 0 && ok && a.snaps != nullptr && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
       if constexpr (CAUSAL) {
         m_tok0 = ok ? a.chunk_tok0[cc] : 0;
         m_len = ok ? a.chunk_len[cc] : 0;
@@ -128,12 +160,12 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   auto load = [&](int c, F& f) {
     meta(c, f);
     const size_t unit = (size_t)c * H + h;
-    const __bf16* Wp = a.in.W + unit * (size_t)(C * K);
+    const _Float16* Wp = a.in.W + unit * (size_t)(C * K);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const size_t fo = ((size_t)(w * KS + s) * 64 + lane) * 8;
-      f.w[s] = *(const bf16x8*)(Wp + fo);
-      if constexpr (CAUSAL) f.qg[s] = *(const bf16x8*)(a.in.qg + unit * (size_t)(C * K) + fo);
+      f.w[s] = *(const f16x8*)(Wp + fo);
+      if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + unit * (size_t)(C * K) + fo);
     }
     const _Float16* Kp = a.in.kgT + unit * (size_t)(C * K);
     const float* dp = a.in.decay + unit * K;
@@ -149,10 +181,15 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) f.aq[s] = *(const f16x8*)(Ap + ((size_t)(w * 2 + s) * 64 + lane) * 8);
     }
-    const _Float16* Up = a.in.U + unit * (size_t)(C * V);
+    if constexpr (MODE != 1) {
+      const _Float16* Up = a.in.U + unit * (size_t)(C * V);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-      f.u[ct] = *(const f16x4*)(Up + ((size_t)(w * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
+      for (int ct = 0; ct < CT; ++ct)
+        f.u[ct] = *(const f16x4*)(Up + ((size_t)(w * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) f.u[ct] = f16x4{};
+    }
   };
 
   // B operand of a P-frag product: rows {32s + 4lg + e} and {32s + 16 + 4lg + e}
@@ -191,9 +228,9 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const bf16x8 sb = b_operand(S_lds, SKP, ct, s);
-        acc[ct] = mfma_bf16(f.w[s], sb, acc[ct]);
-        if constexpr (CAUSAL) acco[ct] = mfma_bf16(f.qg[s], sb, acco[ct]);
+        const f16x8 sb = b_operand(S_lds, SKP, ct, s);
+        acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
+        if constexpr (CAUSAL) acco[ct] = mfma_f16(f.qg[s], sb, acco[ct]);
       }
     }
 #pragma unroll
@@ -260,7 +297,11 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
     }
   }
 
-  if (a.ht != nullptr) {
+  float* out = nullptr;
+  if constexpr (MODE == 1) out = a.grp.P + ((size_t)unitg * H + h) * K * K;
+  else if constexpr (MODE == 2) out = a.grp.Q + ((size_t)unitg * H + h) * K * V;
+  else if (last && a.ht != nullptr) out = a.ht + ((size_t)seq * H + h) * K * V;
+  if (out != nullptr) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -268,18 +309,198 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = 16 * (w * RT + rt) + 4 * lg + e;
-          a.ht[state_off + (size_t)row * V + v0 + 16 * ct + lr] = S[rt][ct][e];
+          out[(size_t)row * NC + v0 + 16 * ct + lr] = S[rt][ct][e];
         }
+  }
+}
+
+// Group table of the two-level scan: sequence n's chunks [c0, c1) form
+// ceil((c1 - c0) / L) groups of L chunks (the last one shorter).  One workgroup.
+__global__ __launch_bounds__(256) void group_table_kernel(const int32_t* __restrict__ seq_chunk_offsets, int n_seq,
+                                                          int L, int32_t* __restrict__ seq_group_offsets,
+                                                          int32_t* __restrict__ group_chunk_offsets,
+                                                          int32_t* __restrict__ group_seq) {
+  __shared__ int scan_s[256];
+  __shared__ int carry_s;
+  const int tid = threadIdx.x;
+  if (tid == 0) carry_s = 0;
+  __syncthreads();
+  for (int base = 0; base < n_seq; base += 256) {
+    const int n = base + tid;
+    const int c0 = n < n_seq ? seq_chunk_offsets[n] : 0;
+    const int c1 = n < n_seq ? seq_chunk_offsets[n + 1] : 0;
+    const int cnt = n < n_seq ? (c1 - c0 + L - 1) / L : 0;
+    scan_s[tid] = cnt;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int add = tid >= off ? scan_s[tid - off] : 0;
+      __syncthreads();
+      scan_s[tid] += add;
+      __syncthreads();
+    }
+    const int first = carry_s + scan_s[tid] - cnt;
+    if (n < n_seq) {
+      seq_group_offsets[n] = first;
+      for (int j = 0; j < cnt; ++j) {
+        group_chunk_offsets[first + j] = c0 + j * L;
+        group_seq[first + j] = n;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) carry_s += scan_s[255];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    seq_group_offsets[n_seq] = carry_s;
+    group_chunk_offsets[carry_s] = seq_chunk_offsets[n_seq];
+  }
+}
+
+// Phase 2 of the two-level scan, one workgroup per (sequence, head, 32 state
+// columns): S_{g+1} = P_g S_g + Q_g over the sequence's groups, writing the state
+// entering every group but the first.  P_g S_g is split-bf16 MFMA
+// (P_hi S_hi + P_hi S_lo + P_lo S_hi) with fp32 accumulation; P and Q of the
+// next group are prefetched while the current one is applied.
+template <int K, int V>
+struct CombineFrag {
+  static constexpr int RT = K / 64, KS = K / 32;
+  f32x4 p[RT][KS][2];
+  f32x4 q[RT][2];
+};
+
+template <int K, int V>
+__global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
+  using F = CombineFrag<K, V>;
+  constexpr int BV = 32, NV = V / BV, RT = F::RT, KS = F::KS, CT = 2, SP = K + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 Shi[BV * SP];
+  __shared__ __attribute__((aligned(16))) __bf16 Slo[BV * SP];
+  const int H = a.H;
+  const int vs = blockIdx.x % NV, h = (blockIdx.x / NV) % H, n = blockIdx.x / (NV * H);
+  const int g0 = a.grp.seq_group_offsets[n], g1 = a.grp.seq_group_offsets[n + 1];
+  if (g1 - g0 <= 1) return;
+  const int v0 = vs * BV, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+
+  f32x4 S[RT][CT];
+  const float* h0p = a.h0 ? a.h0 + ((size_t)n * H + h) * K * V : nullptr;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * (w * RT + rt) + 4 * lg + e;
+        S[rt][ct][e] = h0p ? h0p[(size_t)row * V + v0 + 16 * ct + lr] : 0.f;
+      }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): settle h0 before the prefetching loop
+  asm volatile("" ::: "memory");
+
+  auto load = [&](int g, F& f) {
+    const float* P = a.grp.P + ((size_t)g * H + h) * K * K;
+    const float* Q = a.grp.Q + ((size_t)g * H + h) * K * V;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = 16 * (w * RT + rt) + lr;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        f.p[rt][s][0] = *(const f32x4*)(P + (size_t)row * K + 32 * s + 8 * lg);
+        f.p[rt][s][1] = *(const f32x4*)(P + (size_t)row * K + 32 * s + 8 * lg + 4);
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          f.q[rt][ct][e] = Q[(size_t)(16 * (w * RT + rt) + 4 * lg + e) * V + v0 + 16 * ct + lr];
+    }
+  };
+  auto step = [&](int g, const F& f) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hi[e] = (__bf16)S[rt][ct][e];
+          lo[e] = (__bf16)(S[rt][ct][e] - (float)hi[e]);
+        }
+        const int off = (16 * ct + lr) * SP + 16 * (w * RT + rt) + 4 * lg;
+        *(bf16x4*)(&Shi[off]) = hi;
+        *(bf16x4*)(&Slo[off]) = lo;
+      }
+    lds_barrier();
+    f32x4 acc[RT][CT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = zero4();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 bh[CT], bl[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        bh[ct] = *(const bf16x8*)(&Shi[(16 * ct + lr) * SP + 32 * s + 8 * lg]);
+        bl[ct] = *(const bf16x8*)(&Slo[(16 * ct + lr) * SP + 32 * s + 8 * lg]);
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        bf16x8 ph, pl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float pv = f.p[rt][s][i >> 2][i & 3];
+          ph[i] = (__bf16)pv;
+          pl[i] = (__bf16)(pv - (float)ph[i]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          acc[rt][ct] = mfma_bf16(ph, bh[ct], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf16(ph, bl[ct], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf16(pl, bh[ct], acc[rt][ct]);
+        }
+      }
+    }
+    float* S0 = a.grp.S0 + ((size_t)(g + 1) * H + h) * K * V;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          S[rt][ct][e] = acc[rt][ct][e] + f.q[rt][ct][e];
+          S0[(size_t)(16 * (w * RT + rt) + 4 * lg + e) * V + v0 + 16 * ct + lr] = S[rt][ct][e];
+        }
+    lds_barrier();
+  };
+  // groups g0 .. g1 - 2 each produce the start state of the next group
+  const int glast = g1 - 2;
+  F fa, fb;
+  load(g0, fa);
+  load(min(g0 + 1, glast), fb);
+  for (int g = g0; g <= glast; g += 2) {
+    step(g, fa);
+    load(min(g + 2, glast), fa);
+    if (g + 1 > glast) break;
+    step(g + 1, fb);
+    load(min(g + 3, glast), fb);
   }
 }
 
 template <int K, int V, int BV>
 hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
-  dim3 grid((V / BV) * a.H * a.n_seq), block(256);
+  const dim3 block(256);
+  int units = a.n_seq;
+  if (a.group_L > 0) {
+    units = group_bound(a.n_chunk, a.n_seq, a.group_L);
+    hipLaunchKernelGGL(group_table_kernel, dim3(1), block, 0, stream, a.seq_chunk_offsets, a.n_seq, a.group_L,
+                       a.grp.seq_group_offsets, a.grp.group_chunk_offsets, a.grp.group_seq);
+    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 1>), dim3((K / BV) * a.H * units), block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 2>), dim3((V / BV) * a.H * units), block, 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), block, 0, stream, a);
+  }
+  const dim3 grid((V / BV) * a.H * units);
   if (causal)
-    hipLaunchKernelGGL((state_kernel<K, V, BV, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, BV, true, 0>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((state_kernel<K, V, BV, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 0>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

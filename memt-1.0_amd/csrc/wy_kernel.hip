@@ -24,16 +24,16 @@
 //   factors   fa = 2^(gk - gk_start) <= 1 and 1/fa, with gk_start the cumulative decay at
 //             the first token of the lane's block; per-channel block factors in LDS.
 //   L, Aqk    16x16 tiles, computed transposed so that each lane holds one row.
-//             Diagonal tiles: split-bf16 MFMA (hi*hi + hi*lo + lo*hi) of (b k fa) and
-//             (k / fa): fp32 range and ~2^-16 relative precision.  Off-diagonal tiles
+//             Diagonal tiles: fp32 MFMA of (b k fa) and (k / fa), exact products in
+//             fp32 range.  Off-diagonal tiles
 //             (J < I): fp16 MFMA of (b k fa) and k 2^(gk_start(I) - gk) <= 1, the latter
 //             built by wave J.  A block whose in-block decay exceeds 2^96 forms its
 //             diagonal tile from exact pairwise factors instead (wave-local shuffles).
 //   inverse   A_II by row-wise substitution (fp32), then
 //             A_IJ = -A_II sum_{J<=M<I} L_IM A_MJ with fp32 MFMA, through LDS.
-//   W, U      bf16 / fp16 MFMA against column-major xw / xu tiles in LDS, staged by an
+//   W, U      fp16 MFMA against column-major xw / xu tiles in LDS, staged by an
 //             exact identity-matrix MFMA transpose of each wave's rows.
-// Precision: the erase path (W, b k 2^gk) is bf16; the value path (beta v, A, U,
+// Precision: every MFMA operand of the state scan (W, b k 2^gk, qg, beta v, A, U,
 // kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.
 // LDS stays under 80 KB at d = 128, so two workgroups share a CU.
 #include "gdn2_internal.h"
@@ -66,14 +66,15 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
   // per channel: rows 0-3 gk at the block starts, 4-6 2^(start_{w+1} - start_w),
   // 7-10 2^(gk_last - start_w), 11-14 2^start_w, 15 gk_last
   __shared__ __attribute__((aligned(16))) float fac_s[16 * K];
-  __shared__ __attribute__((aligned(16))) _Float16 xch_s[XCH];   // off-diagonal operands, then xw (bf16)
+  __shared__ __attribute__((aligned(16))) _Float16 xch_s[XCH];   // off-diagonal operands, then xw
   __shared__ __attribute__((aligned(16))) _Float16 xu_s[V * XP];  // column-major beta v
   __shared__ __attribute__((aligned(16))) float As_s[C * AP];     // A, row-major
   __shared__ __attribute__((aligned(16))) float Ld_s[4 * 16 * LQ];
-  __bf16* const xw_s = (__bf16*)xch_s;
+  _Float16* const xw_s = xch_s;
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int tok0 = a.chunk_tok0[chunk], len = a.chunk_len[chunk];
   const size_t unit = (size_t)chunk * H + h;
   const int t = 16 * wave + lr;
@@ -90,13 +91,17 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int c0 = 32 * s + 16 * half + 4 * lg;
-      bf16x4 kk{}, bb{}, qq{};
-      f32x4 gg = zero4();
-      if (valid) {
-        kk = *(const bf16x4*)(a.k + rowK + c0);
-        if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
-        if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
-        gg = *(const f32x4*)(a.g + rowK + c0);
+      // rows past the chunk end read row 0 of the chunk and are zeroed below
+      bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
+      bf16x4 bb{}, qq{};
+      if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
+      if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
+      f32x4 gg = *(const f32x4*)(a.g + rowK + c0);
+      if (!valid) {
+        kk = bf16x4{};
+        bb = bf16x4{};
+        qq = bf16x4{};
+        gg = zero4();
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -115,17 +120,18 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int c0 = 32 * s + 16 * half + 4 * lg;
-      bf16x4 vv{};
-      f32x4 bt = zero4();
-      if (valid) {
-        vv = *(const bf16x4*)(a.v + rowV + c0);
-        if constexpr (sizeof(BetaT) == 4) {
-          bt = *(const f32x4*)((const float*)a.beta + rowV + c0);
-        } else {
-          const bf16x4 b4 = *(const bf16x4*)((const __bf16*)a.beta + rowV + c0);
+      bf16x4 vv = *(const bf16x4*)(a.v + rowV + c0);
+      f32x4 bt;
+      if constexpr (sizeof(BetaT) == 4) {
+        bt = *(const f32x4*)((const float*)a.beta + rowV + c0);
+      } else {
+        const bf16x4 b4 = *(const bf16x4*)((const __bf16*)a.beta + rowV + c0);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) bt[e] = (float)b4[e];
-        }
+        for (int e = 0; e < 4; ++e) bt[e] = (float)b4[e];
+      }
+      if (!valid) {
+        vv = bf16x4{};
+        bt = zero4();
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) xu8[s][4 * half + e] = (_Float16)((float)vv[e] * bt[e]);
@@ -136,14 +142,12 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
   // is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
   // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
   f16x8 sel_h[2];
-  bf16x8 sel_b[2];
 #pragma unroll
   for (int half = 0; half < 2; ++half)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const bool one = (j >> 2) == half && 4 * lg + (j & 3) == lr;
       sel_h[half][j] = (_Float16)(one ? 1.f : 0.f);
-      sel_b[half][j] = (__bf16)(one ? 1.f : 0.f);
     }
   // beta v to LDS now, column-major (channel rows, token columns)
 #pragma unroll
@@ -189,8 +193,10 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
         for (int e = 0; e < 4; ++e) gk[s][4 * half + e] = lv[e];
       }
     }
-  if (tid < K) {
-    const int c = tid;
+  if (tid < 2 * K) {
+    // two threads per channel: part 0 writes the block starts, their ratios and gk_last,
+    // part 1 the powers used by kg and by xw / qg
+    const int c = tid % K, part = tid / K;
     float ref[4], last;
     if constexpr (!G_CUM) {
       // same summation order as the per-lane offsets above, so fa == 1 exactly at block starts
@@ -206,15 +212,21 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
 #pragma unroll
       for (int w2 = 0; w2 < 4; ++w2) ref[w2] = (16 * w2 < len) ? first_s[w2 * K + c] : last;
     }
+    if (part == 0) {
 #pragma unroll
-    for (int w2 = 0; w2 < 4; ++w2) {
-      fac_s[w2 * K + c] = ref[w2];
-      if (w2 < 3) fac_s[(4 + w2) * K + c] = fast_exp2(ref[w2 + 1] - ref[w2]);
-      fac_s[(7 + w2) * K + c] = fast_exp2(last - ref[w2]);
-      fac_s[(11 + w2) * K + c] = fast_exp2(ref[w2]);
+      for (int w2 = 0; w2 < 4; ++w2) {
+        fac_s[w2 * K + c] = ref[w2];
+        if (w2 < 3) fac_s[(4 + w2) * K + c] = fast_exp2(ref[w2 + 1] - ref[w2]);
+      }
+      fac_s[15 * K + c] = last;
+      a.out.decay[unit * K + c] = fast_exp2(last);
+    } else {
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        fac_s[(7 + w2) * K + c] = fast_exp2(last - ref[w2]);
+        fac_s[(11 + w2) * K + c] = fast_exp2(ref[w2]);
+      }
     }
-    fac_s[15 * K + c] = last;
-    a.out.decay[unit * K + c] = fast_exp2(last);
   }
   lds_barrier();
 
@@ -267,12 +279,12 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
   // k 2^(start_I - gk) = k (1/fa) prod_{w=J}^{I-1} 2^(start_{w+1} - start_w), each factor <= 1.
   auto pair_index = [](int I, int J) { return J * (7 - J) / 2 + (I - J - 1); };
   f16x8 a16[KS], aq16[CAUSAL ? KS : 1];
-  bf16x8 xw8[KS];
+  f16x8 xw8[KS];
   _Float16* const kg_out = a.out.kgT + unit * (size_t)(C * K);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    bf16x8 ahi, alo, khi, klo, qhi, qlo, qg8;
-    f16x8 kg8;
+    f16x8 qg8, kg8;
+    float avs[8], kbs[8], qvs[8];
     float base[8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -290,36 +302,31 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
         const float d = gk[s][j] - r4[e];  // <= 0
         const float fa = fast_exp2(d), ifa = fast_exp2(-d);
         const float av = bkf(s, j) * fa;
-        ahi[j] = (__bf16)av;
-        alo[j] = (__bf16)(av - (float)ahi[j]);
+        avs[j] = av;
         a16[s][j] = (_Float16)av;
-        xw8[s][j] = (__bf16)(av * ew[e]);
+        xw8[s][j] = (_Float16)(av * ew[e]);
         const float kbv = kf(s, j) * ifa;
-        khi[j] = (__bf16)kbv;
-        klo[j] = (__bf16)(kbv - (float)khi[j]);
+        kbs[j] = kbv;
         kg8[j] = (_Float16)(wide ? kf(s, j) * fast_exp2(lastv[e] - gk[s][j]) : kbv * gw[e]);
         base[j] = kf(s, j) * (wide ? fast_exp2(rn[e] - gk[s][j]) : ifa * dj[e]);
         if constexpr (CAUSAL) {
           const float qv = qf(s, j) * fa;
-          qhi[j] = (__bf16)qv;
-          qlo[j] = (__bf16)(qv - (float)qhi[j]);
+          qvs[j] = qv;
           aq16[s][j] = (_Float16)qv;
-          qg8[j] = (__bf16)(qv * ew[e]);
+          qg8[j] = (_Float16)(qv * ew[e]);
         }
       }
     }
     if (!wide) {
-      Ld4 = mfma_bf16(khi, ahi, Ld4);
-      Ld4 = mfma_bf16(khi, alo, Ld4);
-      Ld4 = mfma_bf16(klo, ahi, Ld4);
-      if constexpr (CAUSAL) {
-        Qd4 = mfma_bf16(khi, qhi, Qd4);
-        Qd4 = mfma_bf16(khi, qlo, Qd4);
-        Qd4 = mfma_bf16(klo, qhi, Qd4);
+      // fp32 MFMA, one channel per lane group and step: exact products, full range
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        Ld4 = mfma_f32(kbs[j], avs[j], Ld4);
+        if constexpr (CAUSAL) Qd4 = mfma_f32(kbs[j], qvs[j], Qd4);
       }
     }
     if constexpr (CAUSAL)
-      *(bf16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + s) * 64 + lane) * 8) = qg8;
+      *(f16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + s) * 64 + lane) * 8) = qg8;
     // kg^T to global as P-frags (rows = channels, reduction = tokens)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -427,11 +434,11 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
   // xw, column-major (channel rows, token columns), by identity transposes
 #pragma unroll
   for (int ct = 0; ct < KT; ++ct) {
-    const f32x4 tr = mfma_bf16(xw8[ct >> 1], sel_b[ct & 1], zero4());
-    bf16x4 o4;
+    const f32x4 tr = mfma_f16(xw8[ct >> 1], sel_h[ct & 1], zero4());
+    f16x4 o4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = (__bf16)tr[e];
-    *(bf16x4*)(&xw_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
+    for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
+    *(f16x4*)(&xw_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
   }
 
   // ---- A_IJ = -A_II sum_{M=J}^{I-1} L_IM A_MJ, stage d = I - J ----
@@ -458,11 +465,10 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
     lds_barrier();
   }
 
-  // ---- W^T = xw^T A^T (bf16) and U = A xu (fp16), row block R = wave ----
+  // ---- W^T = xw^T A^T and U = A xu (fp16), row block R = wave ----
   {
     const int R = wave;
     constexpr int NS = 2;  // 32-token reduction steps
-    bf16x8 ab[NS];
     f16x8 ah[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -470,30 +476,27 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
       for (int half = 0; half < 2; ++half) {
         const f32x4 r4 = *(const f32x4*)(&As_s[(16 * R + lr) * AP + 32 * s + 16 * half + 4 * lg]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ab[s][4 * half + e] = (__bf16)r4[e];
-          ah[s][4 * half + e] = (_Float16)r4[e];
-        }
+        for (int e = 0; e < 4; ++e) ah[s][4 * half + e] = (_Float16)r4[e];
       }
     }
     const bool two = R >= 2;  // row blocks 0, 1 have no entries past token 31
-    __bf16* W_out = a.out.W + unit * (size_t)(C * K);
+    _Float16* W_out = a.out.W + unit * (size_t)(C * K);
 #pragma unroll
     for (int ct = 0; ct < KT; ++ct) {
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         if (s == 1 && !two) continue;
-        const __bf16* col = xw_s + (16 * ct + lr) * XP + 32 * s + 4 * lg;
-        const bf16x4 lo = *(const bf16x4*)col;
-        const bf16x4 hi = *(const bf16x4*)(col + 16);
-        const bf16x8 xa{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc = mfma_bf16(xa, ab[s], acc);
+        const _Float16* col = xw_s + (16 * ct + lr) * XP + 32 * s + 4 * lg;
+        const f16x4 lo = *(const f16x4*)col;
+        const f16x4 hi = *(const f16x4*)(col + 16);
+        const f16x8 xa{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc = mfma_f16(xa, ah[s], acc);
       }
-      bf16x4 o4;
+      f16x4 o4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = (__bf16)acc[e];
-      *(bf16x4*)(W_out + ((size_t)(R * KS + (ct >> 1)) * 64 + lane) * 8 + (ct & 1) * 4) = o4;
+      for (int e = 0; e < 4; ++e) o4[e] = (_Float16)acc[e];
+      *(f16x4*)(W_out + ((size_t)(R * KS + (ct >> 1)) * 64 + lane) * 8 + (ct & 1) * 4) = o4;
     }
     _Float16* U_out = a.out.U + unit * (size_t)(C * V);
 #pragma unroll

@@ -33,7 +33,7 @@ OUT_CAUSAL = 2
 CHUNK_BLOCK_START = 1
 CHUNK_COMMIT = 2
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Plan(ctypes.Structure):
@@ -65,7 +65,7 @@ _SIGNATURES = {
     "memt_gdn2_strerror": (ctypes.c_char_p, [_I]),
     "memt_gdn2_l2norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _F, _P]),
     "memt_gdn2_chunk_local_cumsum": (_I, [_P, _I, _P, _PLAN, _I, _I, _F, _I, _P]),
-    "memt_gdn2_chunk_update_workspace_size": (_SZ, [_I, _I, _I, _I, _I]),
+    "memt_gdn2_chunk_update_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "memt_gdn2_chunk_update": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],

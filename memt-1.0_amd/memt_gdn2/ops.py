@@ -41,9 +41,10 @@ def _contig(*ts):
     return [None if t is None else t.contiguous() for t in ts]
 
 
-def workspace_bytes(num_chunk: int, H: int, K: int, V: int, out_mode: str = "snapshot") -> int:
-    """Device workspace of one chunked update (fragments of W, kg, U, ...)."""
-    return int(_lib.load().memt_gdn2_chunk_update_workspace_size(num_chunk, H, K, V, _OUT[out_mode]))
+def workspace_bytes(num_chunk: int, H: int, K: int, V: int, out_mode: str = "snapshot", num_seq: int = 1) -> int:
+    """Device workspace of one chunked update (fragments of W, kg, U, ..., and the
+    group states of the two-level scan when the sequences are long)."""
+    return int(_lib.load().memt_gdn2_chunk_update_workspace_size(num_chunk, num_seq, H, K, V, _OUT[out_mode]))
 
 
 def _workspace(device, nbytes: int) -> torch.Tensor:
@@ -191,7 +192,7 @@ def memt_gdn2_fwd_h(kg, w_wy, u_wy, gk, plan: ChunkPlan, initial_state=None, out
     dev = kg.device
     snaps = torch.zeros(plan.num_block, H, K, V, dtype=torch.float32, device=dev)
     final = torch.zeros(plan.num_sample, H, K, V, dtype=torch.float32, device=dev) if output_final_state else None
-    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "none"))
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "none", plan.num_sample))
     p = plan.abi()
     _lib.check(
         lib.memt_gdn2_fwd_h(kg.data_ptr(), w_wy.data_ptr(), u_wy.data_ptr(), gk.data_ptr(), ctypes.byref(p), T, H, K,
@@ -266,7 +267,7 @@ def _chunk_update(q, k, v, g, beta, b, h0, read_states, plan: ChunkPlan, scale: 
     dev = k.device
     final = torch.empty(plan.num_sample, H, K, V, dtype=torch.float32, device=dev) if want_final else None
     o = torch.empty(1, T, H, V, dtype=torch.bfloat16, device=dev) if out_mode != "none" else None
-    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, out_mode))
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, out_mode, plan.num_sample))
     p = plan.abi()
     _lib.check(
         lib.memt_gdn2_chunk_update(

@@ -34,8 +34,8 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.memt_gdn2_abi_version() == 1
-    assert int(re.search(r"#define MEMT_GDN2_ABI_VERSION (\d+)", HEADER.read_text()).group(1)) == 1
+    assert lib.memt_gdn2_abi_version() == _lib.ABI_VERSION
+    assert int(re.search(r"#define MEMT_GDN2_ABI_VERSION (\d+)", HEADER.read_text()).group(1)) == _lib.ABI_VERSION
     for code in (0, -1, -2, -3, -4):
         assert lib.memt_gdn2_strerror(code)
     assert lib.memt_gdn2_strerror(-99) == b"unknown status"
@@ -73,8 +73,12 @@ def test_host_side_rejections(lib):
     assert lib.memt_gdn2_readout_fused(ptr, None, ptr, ptr, ptr, ptr, 1, 1, 128, 128, 1.0, 1e-6, 0.0, 0,
                                        None) == _lib.EINVAL  # soft cap must be positive
     assert lib.memt_gdn2_rms_norm_gated(ptr, ptr, ptr, ptr, 1, 64, 1e-6, 2.0, 9, None) == _lib.EINVAL
-    assert lib.memt_gdn2_chunk_update_workspace_size(128, 16, 128, 128, 2) > lib.memt_gdn2_chunk_update_workspace_size(
-        128, 16, 128, 128, 1) > 0
+    ws = lib.memt_gdn2_chunk_update_workspace_size
+    assert ws(128, 64, 16, 128, 128, 2) > ws(128, 64, 16, 128, 128, 1) > 0
+    # one long sequence takes the two-level scan, whose group states (transition,
+    # contribution and start state per group and head) add to the workspace
+    extra = ws(128, 1, 16, 128, 128, 2) - ws(128, 64, 16, 128, 128, 2)
+    assert extra >= 8 * 16 * 128 * 128 * 4 * 3
 
 
 def test_python_layer_fails_loudly_without_gpu():
