@@ -124,15 +124,16 @@ struct GroupBuffers {
 };
 
 // Chunks per group for the two-level scan (0 = plain per-sequence scan).
-// Groups are used when the plain scan would occupy few workgroups and the
-// sequences are long; L is the smallest power of two >= 4 that keeps the
-// phase-3 grid near 512 workgroups (two per CU on 256 CUs).
+// The scan runs one workgroup per (sequence or group, head).  Groups are used
+// when the plain scan would occupy fewer than 256 workgroups (one per CU of
+// the MI355X) and the sequences are long; L is the smallest power of two >= 4
+// that keeps the per-group grid within 256 workgroups.
 inline int scan_group_chunks(int n_chunk, int n_seq, int H, int V) {
+  (void)V;
   if (n_seq <= 0 || n_chunk <= 0) return 0;
-  const long slices = V / 32;
-  if ((long)n_seq * H * slices >= 512) return 0;
+  if ((long)n_seq * H >= 256) return 0;
   int L = 4;
-  while ((long)(n_chunk / L) * H * slices > 512 && L < (1 << 20)) L *= 2;
+  while ((long)(n_chunk / L) * H > 256 && L < (1 << 20)) L *= 2;
   if (n_chunk / n_seq < 2 * L) return 0;
   return L;
 }

@@ -1,9 +1,7 @@
 // Inter-chunk state scan of the chunked GDN-2 update.
 //
-// One workgroup (4 waves) per (sequence, head, slice of BV state columns).
-// Columns of the state are independent in the recurrence (v_new[:, j] only
-// depends on S[:, j]), so each workgroup keeps its K x BV fp32 slice of S in
-// MFMA accumulators for the whole sequence and walks the chunks in order
+// One workgroup (8 waves) per (sequence or chunk group, head) holds the head's
+// whole K x NC fp32 state in MFMA accumulators and walks the chunks in order
 // (models/qwen/ops/_triton/state.py:76-115):
 //
 //   snapshot S if the chunk starts a read block
@@ -12,71 +10,63 @@
 //   S     = decay * S + kg^T . f16(V_new)           (value path, if committed)
 // Every product is fp16 MFMA with fp32 accumulation; S stays fp32.
 //
-// Wave w owns S rows [w*K/4, (w+1)*K/4) and V_new / o token rows [16w, 16w+16),
-// so it reads only its quarter of each chunk record.  f16(S) and f16(V_new)
-// cross waves through two column-major LDS tiles, with two LDS-only barriers
-// per chunk.  The W / qg / kg^T / Aqk records are P-frags, whose reduction
-// index pairs with B operands gathered as two 8-byte LDS reads per lane.
+// Wave w = 4 c + q owns state rows [q K/4, (q+1) K/4), token rows [16 q, 16 q + 16)
+// and the column half c.  The two waves of a (q, c) pair on one SIMD read the
+// same chunk record fragments (W / qg / kg^T / Aqk rows of quarter q), so each
+// record is fetched from L2 once per head and chunk and the second read hits
+// the CU's L1.  f16(S) and f16(V_new) cross waves through two column-major
+// LDS tiles, with two LDS-only barriers per chunk.  The records are P-frags,
+// whose reduction index pairs with B operands gathered as two 8-byte LDS reads.
 //
-// Prefetch: everything a chunk needs from global memory (its operand
-// fragments and its plan entries) is loaded into registers two chunks ahead;
-// the loop is unrolled by two so the two register buffers alternate without
-// copies, and the compiler's vmcnt waits stay exact.
+// The causal output is formed transposed (f16(S) and V_new as A operands, qg
+// and Aqk as B operands), so each lane holds 4 consecutive output columns of
+// one token and stores 8 bytes.
+//
+// Prefetch: each record fragment of chunk c + 1 is loaded right after its last
+// use in chunk c (one register buffer); plan entries come from a per-wave
+// cache of 64 chunks.  Loads past the last chunk reload the last chunk, so
+// every load is unconditional and the compiler's vmcnt waits stay exact.
 //
 // Long sequences use a two-level scan over groups of chunks (the recurrence is
-// linear in S): the same kernel first runs on [I | 0] per group to form the
-// group transition P_g and its zero-start contribution Q_g (modes 1 and 2),
-// combine_kernel then chains S_{g+1} = P_g S_g + Q_g per sequence (split-bf16
-// MFMA, ~2^-16 relative), and the scan proper runs per group from S_g.
+// linear in S): the same loop first runs on [I | 0] per group to form the
+// group transition P_g and its zero-start contribution Q_g (modes 1 and 2,
+// trans_kernel), combine_kernel then chains S_{g+1} = P_g S_g + Q_g per
+// sequence (split-bf16 MFMA, ~2^-16 relative), and the scan proper runs per
+// group from S_g.
 #include "gdn2_internal.h"
 
 namespace memt {
 namespace {
 
-template <int K, int V, int BV, bool CAUSAL>
+template <int K, int NC, bool CAUSAL>
 struct ScanFrag {
   static constexpr int KS = K / 32;
-  static constexpr int RT = K / 64;   // 16-row S tiles per wave
-  static constexpr int CT = BV / 16;  // 16-column tiles per workgroup
+  static constexpr int RT = K / 64;    // 16-row state tiles per wave
+  static constexpr int CT = NC / 32;   // 16-column tiles per wave (half the columns)
   f16x8 w[KS];
   f16x8 qg[CAUSAL ? KS : 1];
   f16x8 kg[RT][2];
   f16x8 aq[CAUSAL ? 2 : 1];
   f16x4 u[CT];
   f32x4 d[RT];
-  int flags, block, tok0, len;
 };
 
-// MODE 0: the scan (per sequence, or per group from its start state)
-// MODE 1: group transition P_g, columns of the K x K identity, no values
-// MODE 2: group contribution Q_g, value columns from a zero state
-template <int K, int V, int BV, bool CAUSAL, int MODE>
-__global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
-  using F = ScanFrag<K, V, BV, CAUSAL>;
+constexpr int kScanThreads = 512;
+
+// MODE 0: the scan (per sequence, or per group from its start state), NC = V
+// MODE 1: group transition P_g, columns of the K x K identity, no values, NC = K
+// MODE 2: group contribution Q_g, value columns from a zero state, NC = V
+template <int K, int V, int NC, bool CAUSAL, int MODE>
+__device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, _Float16* S_lds,
+                                          _Float16* Vn_lds) {
+  using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
-  constexpr int NC = MODE == 1 ? K : V;  // state columns of this mode
-  constexpr int NV = NC / BV;
-  static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
-  constexpr int KS = F::KS;
-  constexpr int RT = F::RT;
-  constexpr int CT = F::CT;
+  constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
   constexpr int SKP = K + 8;  // pitch of column-major f16(S)
   constexpr int VNP = C + 8;  // pitch of column-major f16(V_new)
+  static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
   static_assert(RT >= 1 && CT >= 1, "tile shape");
-
-  __shared__ __attribute__((aligned(16))) _Float16 S_lds[BV * SKP];
-  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[BV * VNP];
-
-  // XCD-aware order: the NV slices of one (sequence, head) share an XCD (and its L2),
-  // since they all read the same per-chunk records.
-  const int total = gridDim.x;
-  int bid = blockIdx.x;
-  if ((total & 7) == 0) bid = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int vs = bid % NV;
-  const int h = (bid / NV) % a.H;
-  const int unitg = bid / (NV * a.H);  // sequence, or group when grouped
   const int H = a.H;
-  const int v0 = vs * BV;  // first state column (of P for MODE 1, of V otherwise)
 
   int c_begin, c_end, seq = unitg;
   bool first = true, last = true;
@@ -93,10 +83,13 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
     if (MODE != 0 && last) return;  // the last group's transition is never used
   }
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = w & 3, half = w >> 2;
   const int lr = lane & 15, lg = lane >> 4;
+  const int col0 = half * (NC / 2);  // first state column of this wave
 
-  // S tile rt of this wave: rows 16*(w*RT + rt) + 4*lg + e, column v0 + 16*ct + lr
+  // S tile (rt, ct): rows 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr
   f32x4 S[RT][CT];
   const float* h0p = nullptr;
   if constexpr (MODE == 0) {
@@ -109,8 +102,8 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int row = 16 * (w * RT + rt) + 4 * lg + e;
-        const int col = v0 + 16 * ct + lr;
+        const int row = 16 * (q * RT + rt) + 4 * lg + e;
+        const int col = col0 + 16 * ct + lr;
         if constexpr (MODE == 1) S[rt][ct][e] = row == col ? 1.f : 0.f;
         else S[rt][ct][e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
       }
@@ -127,7 +120,7 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
         f16x4 b4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) b4[e] = (_Float16)S[rt][ct][e];
-        *(f16x4*)(&S_lds[(16 * ct + lr) * SKP + 16 * (w * RT + rt) + 4 * lg]) = b4;
+        *(f16x4*)(&S_lds[(col0 + 16 * ct + lr) * SKP + 16 * (q * RT + rt) + 4 * lg]) = b4;
       }
   };
 
@@ -137,7 +130,8 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
   // outstanding prefetch; this way the wait comes once per 64 chunks.
   int mbase = c_begin - 64;
   int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0;
-  auto meta = [&](int c, F& f) {
+  int flags = 0, block = -1, tok0 = 0, len = 0;
+  auto meta = [&](int c) {
     if (c - mbase >= 64) {
       mbase = c;
       const int cc = c + lane;
@@ -151,149 +145,157 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     const int i = c - mbase;
-    f.flags = __builtin_amdgcn_readlane(m_flags, i);
-    f.block = __builtin_amdgcn_readlane(m_block, i);
-    f.tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
-    f.len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
+    flags = __builtin_amdgcn_readlane(m_flags, i);
+    block = __builtin_amdgcn_readlane(m_block, i);
+    tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
+    len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
   };
 
-  auto load = [&](int c, F& f) {
-    meta(c, f);
+  F f;
+  // fragments used by the V_new / qg . S products
+  auto load_a = [&](int c) {
     const size_t unit = (size_t)c * H + h;
-    const _Float16* Wp = a.in.W + unit * (size_t)(C * K);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const size_t fo = ((size_t)(w * KS + s) * 64 + lane) * 8;
-      f.w[s] = *(const f16x8*)(Wp + fo);
-      if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + unit * (size_t)(C * K) + fo);
-    }
-    const _Float16* Kp = a.in.kgT + unit * (size_t)(C * K);
-    const float* dp = a.in.decay + unit * K;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int rtile = w * RT + rt;
-      f.d[rt] = *(const f32x4*)(dp + 16 * rtile + 4 * lg);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) f.kg[rt][s] = *(const f16x8*)(Kp + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
-    }
-    if constexpr (CAUSAL) {
-      const _Float16* Ap = a.in.Aqk + unit * (size_t)(C * C);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) f.aq[s] = *(const f16x8*)(Ap + ((size_t)(w * 2 + s) * 64 + lane) * 8);
+      const size_t fo = unit * (size_t)(C * K) + ((size_t)(q * KS + s) * 64 + lane) * 8;
+      f.w[s] = *(const f16x8*)(a.in.W + fo);
+      if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + fo);
     }
     if constexpr (MODE != 1) {
-      const _Float16* Up = a.in.U + unit * (size_t)(C * V);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
-        f.u[ct] = *(const f16x4*)(Up + ((size_t)(w * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
+        f.u[ct] = *(const f16x4*)(a.in.U + unit * (size_t)(C * V) +
+                                  ((size_t)(q * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
     } else {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) f.u[ct] = f16x4{};
     }
   };
-
-  // B operand of a P-frag product: rows {32s + 4lg + e} and {32s + 16 + 4lg + e}
-  // of a column-major tile (column 16*ct + lr), as two 8-byte reads.
-  auto b_operand = [&](const auto* tile, int pitch, int ct, int s) {
-    using T = std::remove_cv_t<std::remove_pointer_t<decltype(tile)>>;
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    typedef T T8 __attribute__((ext_vector_type(8)));
-    const T* col = tile + (16 * ct + lr) * pitch + 32 * s + 4 * lg;
-    const T4 lo = *(const T4*)col;
-    const T4 hi = *(const T4*)(col + 16);
-    return T8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  };
-
-  auto step = [&](const F& f) {
-    if (f.block >= 0 && (f.flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
-      const size_t soff = ((size_t)f.block * H + h) * K * V;
+  // fragments used by the state update and the causal output
+  auto load_b = [&](int c) {
+    const size_t unit = (size_t)c * H + h;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < RT; ++rt) {
+      const int rtile = q * RT + rt;
+      f.d[rt] = *(const f32x4*)(a.in.decay + unit * K + 16 * rtile + 4 * lg);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int row = 16 * (w * RT + rt) + 4 * lg + e;
-            a.snaps[soff + (size_t)row * V + v0 + 16 * ct + lr] = S[rt][ct][e];
-          }
-    }
-    // ---- V_new (and qg . S) for token rows [16w, 16w + 16) ----
-    f32x4 acc[CT], acco[CAUSAL ? CT : 1];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      acc[ct] = zero4();
-      if constexpr (CAUSAL) acco[ct] = zero4();
-    }
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const f16x8 sb = b_operand(S_lds, SKP, ct, s);
-        acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
-        if constexpr (CAUSAL) acco[ct] = mfma_f16(f.qg[s], sb, acco[ct]);
-      }
-    }
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      f16x4 vn;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)f.u[ct][e] - acc[ct][e]);
-      *(f16x4*)(&Vn_lds[(16 * ct + lr) * VNP + 16 * w + 4 * lg]) = vn;
-    }
-    lds_barrier();
-
-    // ---- S = decay * S + kg^T . V_new; causal output ----
-    f16x8 vb[CT][2];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) vb[ct][s] = b_operand(Vn_lds, VNP, ct, s);
-    if (f.flags & MEMT_GDN2_CHUNK_COMMIT) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
-#pragma unroll
-          for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
-        }
-      }
+      for (int s = 0; s < 2; ++s)
+        f.kg[rt][s] = *(const f16x8*)(a.in.kgT + unit * (size_t)(C * K) + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
     }
     if constexpr (CAUSAL) {
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acco[ct][e] *= a.scale;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) acco[ct] = mfma_f16(f.aq[s], vb[ct][s], acco[ct]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = 16 * w + 4 * lg + e;
-          if (t < f.len) a.o[((size_t)(f.tok0 + t) * H + h) * V + v0 + 16 * ct + lr] = (__bf16)acco[ct][e];
-        }
-      }
+      for (int s = 0; s < 2; ++s)
+        f.aq[s] = *(const f16x8*)(a.in.Aqk + unit * (size_t)(C * C) + ((size_t)(q * 2 + s) * 64 + lane) * 8);
     }
-    write_S_lds();
-    lds_barrier();
+  };
+
+  // B operand of a P-frag product: rows {32s + 4lg + e} and {32s + 16 + 4lg + e}
+  // of a column-major tile (column col, 16 * ct + lr), as two 8-byte reads.
+  auto b_operand = [&](const _Float16* tile, int pitch, int col, int s) {
+    const _Float16* p = tile + col * pitch + 32 * s + 4 * lg;
+    const f16x4 lo = *(const f16x4*)p;
+    const f16x4 hi = *(const f16x4*)(p + 16);
+    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
 
   write_S_lds();
   lds_barrier();
-
-  // The prefetches past the last chunk reload the last chunk (in bounds and
-  // unused): unconditional loads keep the compiler's vmcnt waits exact.
   if (c_begin < c_end) {
     const int c_last = c_end - 1;
-    F fa, fb;
-    load(c_begin, fa);
-    load(min(c_begin + 1, c_last), fb);
-    for (int c = c_begin; c < c_end; c += 2) {
-      step(fa);
-      load(min(c + 2, c_last), fa);
-      if (c + 1 >= c_end) break;
-      step(fb);
-      load(min(c + 3, c_last), fb);
+    meta(c_begin);
+    load_a(c_begin);
+    load_b(c_begin);
+    for (int c = c_begin; c < c_end; ++c) {
+      const int cn = min(c + 1, c_last);
+      if constexpr (MODE == 0) {
+        if (block >= 0 && (flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
+          const size_t soff = ((size_t)block * H + h) * K * V;
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int row = 16 * (q * RT + rt) + 4 * lg + e;
+                a.snaps[soff + (size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e];
+              }
+        }
+      }
+      // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
+      f32x4 acc[CT], acco[CAUSAL ? CT : 1];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        acc[ct] = zero4();
+        if constexpr (CAUSAL) acco[ct] = zero4();
+      }
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const f16x8 sb = b_operand(S_lds, SKP, col0 + 16 * ct + lr, s);
+          acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
+          if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
+        }
+      }
+      f16x4 un[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) un[ct] = f.u[ct];
+      const int cur_flags = flags, cur_tok0 = tok0, cur_len = len;
+      meta(cn);
+      load_a(cn);  // W, qg and U of the next chunk
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        f16x4 vn;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)un[ct][e] - acc[ct][e]);
+        *(f16x4*)(&Vn_lds[(col0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
+      }
+      lds_barrier();
+
+      // ---- S = decay * S + kg^T . V_new; causal output ----
+      f16x8 vb[CT][2];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) vb[ct][s] = b_operand(Vn_lds, VNP, col0 + 16 * ct + lr, s);
+      if (cur_flags & MEMT_GDN2_CHUNK_COMMIT) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
+          }
+        }
+      }
+      if constexpr (CAUSAL) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acco[ct][e] *= a.scale;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) acco[ct] = mfma_f16(vb[ct][s], f.aq[s], acco[ct]);
+        }
+      }
+      load_b(cn);  // decay, kg^T and Aqk of the next chunk
+      if constexpr (CAUSAL) {
+        // lane holds o[16 q + lr][col0 + 16 ct + 4 lg + e]
+        const int t = 16 * q + lr;
+        if (t < cur_len) {
+          __bf16* orow = a.o + ((size_t)(cur_tok0 + t) * H + h) * V + col0 + 4 * lg;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            bf16x4 o4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = (__bf16)acco[ct][e];
+            *(bf16x4*)(orow + 16 * ct) = o4;
+          }
+        }
+      }
+      write_S_lds();
+      lds_barrier();
     }
   }
 
@@ -308,10 +310,30 @@ __global__ __launch_bounds__(256) void state_kernel(StateArgs a) {
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = 16 * (w * RT + rt) + 4 * lg + e;
-          out[(size_t)row * NC + v0 + 16 * ct + lr] = S[rt][ct][e];
+          const int row = 16 * (q * RT + rt) + 4 * lg + e;
+          out[(size_t)row * NC + col0 + 16 * ct + lr] = S[rt][ct][e];
         }
   }
+}
+
+template <int K, int V, bool CAUSAL>
+__global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[V * (K + 8)];
+  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[V * (kChunk + 8)];
+  scan_body<K, V, V, CAUSAL, 0>(a, blockIdx.x / a.H, blockIdx.x % a.H, S_lds, Vn_lds);
+}
+
+// Phase 1 of the two-level scan: blocks [0, units H) form P_g, the rest Q_g.
+template <int K, int V>
+__global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int units) {
+  constexpr int NCM = K > V ? K : V;
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[NCM * (K + 8)];
+  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NCM * (kChunk + 8)];
+  const int b = blockIdx.x, per = units * a.H;
+  if (b < per)
+    scan_body<K, V, K, false, 1>(a, b / a.H, b % a.H, S_lds, Vn_lds);
+  else
+    scan_body<K, V, V, false, 2>(a, (b - per) / a.H, (b - per) % a.H, S_lds, Vn_lds);
 }
 
 // Group table of the two-level scan: sequence n's chunks [c0, c1) form
@@ -484,23 +506,21 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   }
 }
 
-template <int K, int V, int BV>
+template <int K, int V>
 hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
-  const dim3 block(256);
   int units = a.n_seq;
   if (a.group_L > 0) {
     units = group_bound(a.n_chunk, a.n_seq, a.group_L);
-    hipLaunchKernelGGL(group_table_kernel, dim3(1), block, 0, stream, a.seq_chunk_offsets, a.n_seq, a.group_L,
+    hipLaunchKernelGGL(group_table_kernel, dim3(1), dim3(256), 0, stream, a.seq_chunk_offsets, a.n_seq, a.group_L,
                        a.grp.seq_group_offsets, a.grp.group_chunk_offsets, a.grp.group_seq);
-    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 1>), dim3((K / BV) * a.H * units), block, 0, stream, a);
-    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 2>), dim3((V / BV) * a.H * units), block, 0, stream, a);
-    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), block, 0, stream, a);
+    hipLaunchKernelGGL((trans_kernel<K, V>), dim3(2 * units * a.H), dim3(kScanThreads), 0, stream, a, units);
+    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), dim3(256), 0, stream, a);
   }
-  const dim3 grid((V / BV) * a.H * units);
+  const dim3 grid(units * a.H), block(kScanThreads);
   if (causal)
-    hipLaunchKernelGGL((state_kernel<K, V, BV, true, 0>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, true>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((state_kernel<K, V, BV, false, 0>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
@@ -508,8 +528,8 @@ hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
 
 hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream_t stream) {
   if (a.n_seq == 0) return hipSuccess;
-  if (K == 64 && V == 64) return launch_t<64, 64, 32>(a, causal, stream);
-  if (K == 128 && V == 128) return launch_t<128, 128, 32>(a, causal, stream);
+  if (K == 64 && V == 64) return launch_t<64, 64>(a, causal, stream);
+  if (K == 128 && V == 128) return launch_t<128, 128>(a, causal, stream);
   return hipErrorInvalidValue;
 }
 
