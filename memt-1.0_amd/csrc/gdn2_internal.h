@@ -113,14 +113,14 @@ struct WyArgs {
 //            and the zero-start contribution Q_g, by running the scan on [I | 0]
 //   phase 2  per sequence (serial over its groups): S_{g+1} = P_g S_g + Q_g
 //   phase 3  per group (in parallel): the scan proper from S_g, with its outputs
-// The group table is built on the device from seq_chunk_offsets.
+// Sequence n owns the global groups [G_n, G_n + ceil(chunks_n / L)), G_n the
+// running sum over earlier sequences; kernels locate their group from
+// seq_chunk_offsets on the fly.
 struct GroupBuffers {
-  int32_t* seq_group_offsets;    // [n_seq + 1]
-  int32_t* group_chunk_offsets;  // [n_group_bound + 1]
-  int32_t* group_seq;            // [n_group_bound]
-  float* P;                      // [n_group_bound, H, K, K]
-  float* Q;                      // [n_group_bound, H, K, V]
-  float* S0;                     // [n_group_bound, H, K, V] state entering each group
+  __bf16* P_hi;  // [n_group_bound, H, K, K] A-frag order (red = K), P_g = P_hi + P_lo
+  __bf16* P_lo;
+  float* Q;      // [n_group_bound, H, K, V] C-frag order (n = V)
+  float* S0;     // [n_group_bound, H, K, V] C-frag order, state entering each group
 };
 
 // Chunks per group for the two-level scan (0 = plain per-sequence scan).
@@ -145,18 +145,14 @@ inline size_t group_layout(size_t base, int n_chunk, int n_seq, int H, int K, in
   if (L == 0) return base;
   const size_t nb = (size_t)group_bound(n_chunk, n_seq, L);
   size_t o = align256(base);
-  const size_t off_sgo = o; o = align256(o + (size_t)(n_seq + 1) * 4);
-  const size_t off_gco = o; o = align256(o + (nb + 1) * 4);
-  const size_t off_gseq = o; o = align256(o + nb * 4);
-  const size_t off_P = o; o = align256(o + nb * H * K * K * 4);
+  const size_t off_Ph = o; o = align256(o + nb * H * K * K * 2);
+  const size_t off_Pl = o; o = align256(o + nb * H * K * K * 2);
   const size_t off_Q = o; o = align256(o + nb * H * K * V * 4);
   const size_t off_S0 = o; o = align256(o + nb * H * K * V * 4);
   if (out != nullptr) {
     char* b = (char*)ws;
-    out->seq_group_offsets = (int32_t*)(b + off_sgo);
-    out->group_chunk_offsets = (int32_t*)(b + off_gco);
-    out->group_seq = (int32_t*)(b + off_gseq);
-    out->P = (float*)(b + off_P);
+    out->P_hi = (__bf16*)(b + off_Ph);
+    out->P_lo = (__bf16*)(b + off_Pl);
     out->Q = (float*)(b + off_Q);
     out->S0 = (float*)(b + off_S0);
   }

@@ -53,6 +53,65 @@ struct ScanFrag {
 
 constexpr int kScanThreads = 512;
 
+// Where global group g of the two-level scan lies: sequence n owns the groups
+// [G_n, G_n + cnt_n), cnt_n = ceil(chunks_n / L), G_n the sum over earlier
+// sequences.  One wave scans the sequences 64 at a time; every lane returns
+// the same values.
+struct GroupLoc {
+  int seq, c_begin, c_end, first_group, n_groups;
+  bool valid;
+};
+__device__ __forceinline__ GroupLoc locate_group(const int32_t* soff, int n_seq, int L, int g) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  for (int n0 = 0; n0 < n_seq; n0 += 64) {
+    const int n = n0 + lane;
+    int c0 = 0, c1 = 0, cnt = 0;
+    if (n < n_seq) {
+      c0 = soff[n];
+      c1 = soff[n + 1];
+      cnt = (c1 - c0 + L - 1) / L;
+    }
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int first = base + incl - cnt;
+    const unsigned long long hit = __ballot(n < n_seq && g >= first && g < first + cnt);
+    if (hit != 0) {
+      const int src = __ffsll((unsigned long long)hit) - 1;
+      GroupLoc r;
+      r.seq = n0 + src;
+      r.first_group = __shfl(first, src, 64);
+      r.n_groups = __shfl(cnt, src, 64);
+      const int sc0 = __shfl(c0, src, 64), sc1 = __shfl(c1, src, 64);
+      r.c_begin = sc0 + (g - r.first_group) * L;
+      r.c_end = min(r.c_begin + L, sc1);
+      r.valid = true;
+      return r;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  GroupLoc r{};
+  r.valid = false;
+  return r;
+}
+// Groups [first, first + count) of sequence n.
+__device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int L, int& first, int& count) {
+  const int lane = threadIdx.x & 63;
+  int sum = 0;
+  for (int n0 = 0; n0 < n; n0 += 64) {
+    const int m = n0 + lane;
+    int cnt = 0;
+    if (m < n) cnt = (soff[m + 1] - soff[m] + L - 1) / L;
+    sum += wave_sum_int(cnt);
+  }
+  first = sum;
+  count = (soff[n + 1] - soff[n] + L - 1) / L;
+}
+
 // MODE 0: the scan (per sequence, or per group from its start state), NC = V
 // MODE 1: group transition P_g, columns of the K x K identity, no values, NC = K
 // MODE 2: group contribution Q_g, value columns from a zero state, NC = V
@@ -74,12 +133,15 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
     c_begin = a.seq_chunk_offsets[seq];
     c_end = a.seq_chunk_offsets[seq + 1];
   } else {
-    if (unitg >= a.grp.seq_group_offsets[a.n_seq]) return;
-    seq = a.grp.group_seq[unitg];
-    c_begin = a.grp.group_chunk_offsets[unitg];
-    c_end = a.grp.group_chunk_offsets[unitg + 1];
-    first = unitg == a.grp.seq_group_offsets[seq];
-    last = unitg + 1 == a.grp.seq_group_offsets[seq + 1];
+    const GroupLoc gl = locate_group(a.seq_chunk_offsets, a.n_seq, a.group_L, unitg);
+    if (!gl.valid) return;
+    seq = __builtin_amdgcn_readfirstlane(gl.seq);
+    c_begin = __builtin_amdgcn_readfirstlane(gl.c_begin);
+    c_end = __builtin_amdgcn_readfirstlane(gl.c_end);
+    const int g_first = __builtin_amdgcn_readfirstlane(gl.first_group);
+    const int g_count = __builtin_amdgcn_readfirstlane(gl.n_groups);
+    first = unitg == g_first;
+    last = unitg + 1 == g_first + g_count;
     if (MODE != 0 && last) return;  // the last group's transition is never used
   }
 
@@ -91,22 +153,28 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 
   // S tile (rt, ct): rows 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr
   f32x4 S[RT][CT];
-  const float* h0p = nullptr;
-  if constexpr (MODE == 0) {
-    if (!first) h0p = a.grp.S0 + ((size_t)unitg * H + h) * K * V;
-    else if (a.h0 != nullptr) h0p = a.h0 + ((size_t)seq * H + h) * K * V;
+  if (MODE == 0 && !first) {
+    // the group's start state from the combine, in C-frag order
+    const float* s0 = a.grp.S0 + ((size_t)unitg * H + h) * K * V;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        S[rt][ct] = *(const f32x4*)(s0 + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
+  } else {
+    const float* h0p = (MODE == 0 && a.h0 != nullptr) ? a.h0 + ((size_t)seq * H + h) * K * V : nullptr;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 16 * (q * RT + rt) + 4 * lg + e;
+          const int col = col0 + 16 * ct + lr;
+          if constexpr (MODE == 1) S[rt][ct][e] = row == col ? 1.f : 0.f;
+          else S[rt][ct][e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
+        }
   }
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 16 * (q * RT + rt) + 4 * lg + e;
-        const int col = col0 + 16 * ct + lr;
-        if constexpr (MODE == 1) S[rt][ct][e] = row == col ? 1.f : 0.f;
-        else S[rt][ct][e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
-      }
   // settle the initial-state loads here: otherwise every later use of S in the
   // loop would wait for all outstanding loads, prefetches included
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -299,11 +367,30 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
     }
   }
 
-  float* out = nullptr;
-  if constexpr (MODE == 1) out = a.grp.P + ((size_t)unitg * H + h) * K * K;
-  else if constexpr (MODE == 2) out = a.grp.Q + ((size_t)unitg * H + h) * K * V;
-  else if (last && a.ht != nullptr) out = a.ht + ((size_t)seq * H + h) * K * V;
-  if (out != nullptr) {
+  if constexpr (MODE == 1) {
+    // P_g split into bf16 hi + lo, in A-frag order (rows = P rows, reduction = P
+    // columns): the A operands of the combine, one contiguous 16-byte load per lane
+    const size_t base = ((size_t)unitg * H + h) * K * K;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const size_t idx = base + afrag_index(16 * (q * RT + rt) + 4 * lg + e, col0 + 16 * ct + lr, K);
+          const __bf16 hi = (__bf16)S[rt][ct][e];
+          a.grp.P_hi[idx] = hi;
+          a.grp.P_lo[idx] = (__bf16)(S[rt][ct][e] - (float)hi);
+        }
+  } else if constexpr (MODE == 2) {
+    float* qo = a.grp.Q + ((size_t)unitg * H + h) * K * V;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        *(f32x4*)(qo + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4) = S[rt][ct];
+  } else if (last && a.ht != nullptr) {
+    float* out = a.ht + ((size_t)seq * H + h) * K * V;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -311,7 +398,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = 16 * (q * RT + rt) + 4 * lg + e;
-          out[(size_t)row * NC + col0 + 16 * ct + lr] = S[rt][ct][e];
+          out[(size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e];
         }
   }
 }
@@ -336,48 +423,6 @@ __global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int un
     scan_body<K, V, V, false, 2>(a, (b - per) / a.H, (b - per) % a.H, S_lds, Vn_lds);
 }
 
-// Group table of the two-level scan: sequence n's chunks [c0, c1) form
-// ceil((c1 - c0) / L) groups of L chunks (the last one shorter).  One workgroup.
-__global__ __launch_bounds__(256) void group_table_kernel(const int32_t* __restrict__ seq_chunk_offsets, int n_seq,
-                                                          int L, int32_t* __restrict__ seq_group_offsets,
-                                                          int32_t* __restrict__ group_chunk_offsets,
-                                                          int32_t* __restrict__ group_seq) {
-  __shared__ int scan_s[256];
-  __shared__ int carry_s;
-  const int tid = threadIdx.x;
-  if (tid == 0) carry_s = 0;
-  __syncthreads();
-  for (int base = 0; base < n_seq; base += 256) {
-    const int n = base + tid;
-    const int c0 = n < n_seq ? seq_chunk_offsets[n] : 0;
-    const int c1 = n < n_seq ? seq_chunk_offsets[n + 1] : 0;
-    const int cnt = n < n_seq ? (c1 - c0 + L - 1) / L : 0;
-    scan_s[tid] = cnt;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int add = tid >= off ? scan_s[tid - off] : 0;
-      __syncthreads();
-      scan_s[tid] += add;
-      __syncthreads();
-    }
-    const int first = carry_s + scan_s[tid] - cnt;
-    if (n < n_seq) {
-      seq_group_offsets[n] = first;
-      for (int j = 0; j < cnt; ++j) {
-        group_chunk_offsets[first + j] = c0 + j * L;
-        group_seq[first + j] = n;
-      }
-    }
-    __syncthreads();
-    if (tid == 0) carry_s += scan_s[255];
-    __syncthreads();
-  }
-  if (tid == 0) {
-    seq_group_offsets[n_seq] = carry_s;
-    group_chunk_offsets[carry_s] = seq_chunk_offsets[n_seq];
-  }
-}
-
 // Phase 2 of the two-level scan, one workgroup per (sequence, head, 32 state
 // columns): S_{g+1} = P_g S_g + Q_g over the sequence's groups, writing the state
 // entering every group but the first.  P_g S_g is split-bf16 MFMA
@@ -386,7 +431,7 @@ __global__ __launch_bounds__(256) void group_table_kernel(const int32_t* __restr
 template <int K, int V>
 struct CombineFrag {
   static constexpr int RT = K / 64, KS = K / 32;
-  f32x4 p[RT][KS][2];
+  bf16x8 ph[RT][KS], pl[RT][KS];
   f32x4 q[RT][2];
 };
 
@@ -397,9 +442,19 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   __shared__ __attribute__((aligned(16))) __bf16 Shi[BV * SP];
   __shared__ __attribute__((aligned(16))) __bf16 Slo[BV * SP];
   const int H = a.H;
-  const int vs = blockIdx.x % NV, h = (blockIdx.x / NV) % H, n = blockIdx.x / (NV * H);
-  const int g0 = a.grp.seq_group_offsets[n], g1 = a.grp.seq_group_offsets[n + 1];
-  if (g1 - g0 <= 1) return;
+  // XCD-aware order: the NV column slices of one (sequence, head) read the same
+  // P_g and Q_g, so they share an XCD (and its L2); blocks are dispatched to
+  // XCDs round-robin by block index.
+  const int total = gridDim.x;
+  int bid = blockIdx.x;
+  if ((total & 7) == 0) bid = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+  const int vs = bid % NV, h = (bid / NV) % H, n = bid / (NV * H);
+  int g0, gcount;
+  sequence_groups(a.seq_chunk_offsets, n, a.group_L, g0, gcount);
+  g0 = __builtin_amdgcn_readfirstlane(g0);
+  gcount = __builtin_amdgcn_readfirstlane(gcount);
+  if (gcount <= 1) return;
+  const int g1 = g0 + gcount;
   const int v0 = vs * BV, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
 
   f32x4 S[RT][CT];
@@ -416,25 +471,33 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): settle h0 before the prefetching loop
   asm volatile("" ::: "memory");
 
+  // First load, in the order the loop consumes and reloads the fragments: the
+  // empty asm statements keep the compiler from reordering the loads, so the
+  // loop's vmcnt waits stay partial on its entry path too.
   auto load = [&](int g, F& f) {
-    const float* P = a.grp.P + ((size_t)g * H + h) * K * K;
+    const size_t pb = ((size_t)g * H + h) * K * K;
     const float* Q = a.grp.Q + ((size_t)g * H + h) * K * V;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int row = 16 * (w * RT + rt) + lr;
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        f.p[rt][s][0] = *(const f32x4*)(P + (size_t)row * K + 32 * s + 8 * lg);
-        f.p[rt][s][1] = *(const f32x4*)(P + (size_t)row * K + 32 * s + 8 * lg + 4);
+      for (int rt = 0; rt < RT; ++rt) {
+        const size_t fo = pb + ((size_t)((w * RT + rt) * KS + s) * 64 + lane) * 8;
+        f.ph[rt][s] = *(const bf16x8*)(a.grp.P_hi + fo);
+        f.pl[rt][s] = *(const bf16x8*)(a.grp.P_lo + fo);
+        asm volatile("" ::: "memory");
       }
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          f.q[rt][ct][e] = Q[(size_t)(16 * (w * RT + rt) + 4 * lg + e) * V + v0 + 16 * ct + lr];
-    }
+      for (int ct = 0; ct < CT; ++ct)
+        f.q[rt][ct] = *(const f32x4*)(Q + ((size_t)((w * RT + rt) * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4);
   };
-  auto step = [&](int g, const F& f) {
+  // One step applies group g from f, reloading each fragment of f for group
+  // gload right after its last use, so the loads spread over the MFMAs and the
+  // rest of the step.
+  auto step = [&](int g, F& f, int gload) {
+    const size_t pb = ((size_t)gload * H + h) * K * K;
+    const float* Qn = a.grp.Q + ((size_t)gload * H + h) * K * V;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -465,45 +528,34 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
       }
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        bf16x8 ph, pl;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float pv = f.p[rt][s][i >> 2][i & 3];
-          ph[i] = (__bf16)pv;
-          pl[i] = (__bf16)(pv - (float)ph[i]);
-        }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-          acc[rt][ct] = mfma_bf16(ph, bh[ct], acc[rt][ct]);
-          acc[rt][ct] = mfma_bf16(ph, bl[ct], acc[rt][ct]);
-          acc[rt][ct] = mfma_bf16(pl, bh[ct], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf16(f.ph[rt][s], bh[ct], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf16(f.ph[rt][s], bl[ct], acc[rt][ct]);
+          acc[rt][ct] = mfma_bf16(f.pl[rt][s], bh[ct], acc[rt][ct]);
         }
+        const size_t fo = pb + ((size_t)((w * RT + rt) * KS + s) * 64 + lane) * 8;
+        f.ph[rt][s] = *(const bf16x8*)(a.grp.P_hi + fo);
+        f.pl[rt][s] = *(const bf16x8*)(a.grp.P_lo + fo);
       }
     }
     float* S0 = a.grp.S0 + ((size_t)(g + 1) * H + h) * K * V;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          S[rt][ct][e] = acc[rt][ct][e] + f.q[rt][ct][e];
-          S0[(size_t)(16 * (w * RT + rt) + 4 * lg + e) * V + v0 + 16 * ct + lr] = S[rt][ct][e];
-        }
+      for (int ct = 0; ct < CT; ++ct) {
+        const size_t qo = ((size_t)((w * RT + rt) * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4;
+        S[rt][ct] = acc[rt][ct] + f.q[rt][ct];
+        *(f32x4*)(S0 + qo) = S[rt][ct];
+        f.q[rt][ct] = *(const f32x4*)(Qn + qo);
+      }
     lds_barrier();
   };
   // groups g0 .. g1 - 2 each produce the start state of the next group
   const int glast = g1 - 2;
-  F fa, fb;
-  load(g0, fa);
-  load(min(g0 + 1, glast), fb);
-  for (int g = g0; g <= glast; g += 2) {
-    step(g, fa);
-    load(min(g + 2, glast), fa);
-    if (g + 1 > glast) break;
-    step(g + 1, fb);
-    load(min(g + 3, glast), fb);
-  }
+  F f;
+  load(g0, f);
+  for (int g = g0; g <= glast; ++g) step(g, f, min(g + 1, glast));
 }
 
 template <int K, int V>
@@ -511,8 +563,6 @@ hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
   int units = a.n_seq;
   if (a.group_L > 0) {
     units = group_bound(a.n_chunk, a.n_seq, a.group_L);
-    hipLaunchKernelGGL(group_table_kernel, dim3(1), dim3(256), 0, stream, a.seq_chunk_offsets, a.n_seq, a.group_L,
-                       a.grp.seq_group_offsets, a.grp.group_chunk_offsets, a.grp.group_seq);
     hipLaunchKernelGGL((trans_kernel<K, V>), dim3(2 * units * a.H), dim3(kScanThreads), 0, stream, a, units);
     hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), dim3(256), 0, stream, a);
   }
