@@ -134,6 +134,38 @@ def bench_readout(dev, steps, warmup, B=64, H=16, D=128, gate_kind="softcap_silu
     return dict(ms_per_launch=ms, gbs=nb / (ms * 1e-3) / 1e9, bytes=nb, nsets=nsets, launches=reps * nsets)
 
 
+COPY_BYTES = 1 << 30  # calibration copy: reads and writes exactly this many bytes
+
+
+def calibrate(dev, T=8192, H=16, D=128, reps=3):
+    """Workload for hardware-counter runs (rocprofv3 --pmc): a device copy of
+    COPY_BYTES (the reference for FETCH_SIZE / WRITE_SIZE per byte), then `reps`
+    update steps and readouts on distinct inputs.  Prints the kernel inventory."""
+    import memt_gdn2
+
+    x = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    sets = [_inputs(T, H, D, D, seed=20261201 + i, dev=dev) for i in range(reps)]
+    for s in sets:
+        memt_gdn2.chunk_gdn2(s["q"], s["k"], s["v"], s["g"], s["beta"], initial_state=s["h0"], out_mode="causal")
+    torch.cuda.synchronize()
+    g = torch.Generator().manual_seed(20261203)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dev, torch.bfloat16)
+    for _ in range(reps):
+        S = (torch.randn(64, H, D, D, generator=g) * 0.02).to(dev)
+        q = torch.nn.functional.normalize(torch.randn(64, H, D, generator=g), dim=-1).to(dev, torch.bfloat16)
+        gate = torch.randn(64, H, D, generator=g).to(dev, torch.bfloat16)
+        memt_gdn2.readout_fused(S, q, gate, w, scale=D ** -0.5, eps=1e-6)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": COPY_BYTES, "update_steps": reps, "readouts": reps,
+                      "update_algorithmic_bytes": update_bytes(T, H, D, D),
+                      "readout_algorithmic_bytes": readout_bytes(64, H, D, D)}))
+
+
 def cpu_baseline_update(T=8192, H=16, D=128, runs=5):
     """The PyTorch-CPU port (oracle/gdn2_torch.py) on the full workload, fp32."""
     from oracle.gdn2_torch import chunked_gdn2_torch
@@ -186,6 +218,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--mode", default="causal", choices=["causal", "snapshot"])
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run the hardware-counter workload (copy of known size, then update steps and readouts)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN-2 memory path is built and measured on a single MI355X "
@@ -200,6 +234,9 @@ def main():
     memt_gdn2.load()
     dev = torch.device("cuda:0")
     T, H, D = 8192, 16, 128
+    if args.calibrate:
+        calibrate(dev, T, H, D)
+        return
 
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)
     snap = bench_update(dev, max(10, args.steps // 2), 2, T, H, D, out_mode="snapshot") if args.mode == "causal" else None

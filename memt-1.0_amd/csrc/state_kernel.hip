@@ -52,6 +52,10 @@ struct ScanFrag {
 };
 
 constexpr int kScanThreads = 512;
+// Column pitches (in elements) of the f16 LDS tiles: K + kSPad for f16(S),
+// 64 + kVPad for f16(V_new), K + kSPad for the combine's bf16 S halves.
+constexpr int kSPad = 4;
+constexpr int kVPad = 4;
 
 // Where global group g of the two-level scan lies: sequence n owns the groups
 // [G_n, G_n + cnt_n), cnt_n = ceil(chunks_n / L), G_n the sum over earlier
@@ -121,8 +125,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
-  constexpr int SKP = K + 8;  // pitch of column-major f16(S)
-  constexpr int VNP = C + 8;  // pitch of column-major f16(V_new)
+  constexpr int SKP = K + kSPad;  // pitch of column-major f16(S)
+  constexpr int VNP = C + kVPad;  // pitch of column-major f16(V_new)
   static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
   static_assert(RT >= 1 && CT >= 1, "tile shape");
   const int H = a.H;
@@ -405,8 +409,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 
 template <int K, int V, bool CAUSAL>
 __global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 S_lds[V * (K + 8)];
-  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[V * (kChunk + 8)];
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[V * (K + kSPad)];
+  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[V * (kChunk + kVPad)];
   scan_body<K, V, V, CAUSAL, 0>(a, blockIdx.x / a.H, blockIdx.x % a.H, S_lds, Vn_lds);
 }
 
@@ -414,8 +418,8 @@ __global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a) {
 template <int K, int V>
 __global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int units) {
   constexpr int NCM = K > V ? K : V;
-  __shared__ __attribute__((aligned(16))) _Float16 S_lds[NCM * (K + 8)];
-  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NCM * (kChunk + 8)];
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[NCM * (K + kSPad)];
+  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NCM * (kChunk + kVPad)];
   const int b = blockIdx.x, per = units * a.H;
   if (b < per)
     scan_body<K, V, K, false, 1>(a, b / a.H, b % a.H, S_lds, Vn_lds);
@@ -438,7 +442,7 @@ struct CombineFrag {
 template <int K, int V>
 __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   using F = CombineFrag<K, V>;
-  constexpr int BV = 32, NV = V / BV, RT = F::RT, KS = F::KS, CT = 2, SP = K + 8;
+  constexpr int BV = 32, NV = V / BV, RT = F::RT, KS = F::KS, CT = 2, SP = K + kSPad;
   __shared__ __attribute__((aligned(16))) __bf16 Shi[BV * SP];
   __shared__ __attribute__((aligned(16))) __bf16 Slo[BV * SP];
   const int H = a.H;
