@@ -52,6 +52,24 @@ def readout_bytes(B, H, K, V):
     return B * H * (4 * K * V + 2 * K + 2 * V + 2 * V) + 2 * V
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_update_h16_t8192_d128_readout_b64.md"
+
+
+def profiled_traffic():
+    """HBM bytes per update step and per readout launch, from the committed
+    FETCH_SIZE/WRITE_SIZE summary (two rocprofv3 --pmc passes over
+    ``bench.py --calibrate``, scaled by the counters of a 1 GiB copy)."""
+    out = {}
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            key, _, val = line.partition(":")
+            if key in ("update_traffic_bytes_per_step", "readout_traffic_bytes_per_launch"):
+                out[key] = int(val)
+    except OSError:
+        pass
+    return out.get("update_traffic_bytes_per_step"), out.get("readout_traffic_bytes_per_launch")
+
+
 def _inputs(T, H, K, V, seed, dev):
     g = torch.Generator().manual_seed(seed)
     q = torch.nn.functional.normalize(torch.randn(1, T, H, K, generator=g), dim=-1)
@@ -243,6 +261,9 @@ def main():
     ro = bench_readout(dev, args.steps, args.warmup)
 
     causal = args.mode == "causal"
+    up_traffic, ro_traffic = profiled_traffic()
+    if not causal:
+        up_traffic = None  # the committed counters cover the causal workload
     ub = update_bytes(T, H, D, D)
     uf = update_flops(T, H, D, D, causal=causal)
     t_up = up["event_ms_mean"] * 1e-3
@@ -276,7 +297,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": up_traffic,
+            "traffic_source": TRAFFIC_PROFILE.name if up_traffic else None,
             "algorithmic_bytes": ub,
             "event_ms_per_launch": up["event_ms_mean"],
             "mfma_frac": uf / t_up / 1e12 / MFMA_BF16_PEAK_TFLOPS,
@@ -288,7 +310,7 @@ def main():
             "unit": "GB/s",
             "us_per_launch": ro["ms_per_launch"] * 1e3,
             "roofline": {"bound": "hbm", "achieved": ro["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": ro["gbs"] / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": ro["bytes"]},
+                         "frac": ro["gbs"] / HBM_PEAK_GBS, "traffic": ro_traffic, "algorithmic_bytes": ro["bytes"]},
             "state_sets_rotated": ro["nsets"],
         },
     }
