@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 2
+#define MEMT_GDN2_ABI_VERSION 3
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -174,6 +174,38 @@ int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void*
                             const void* gate, const void* weight, void* out, int B, int H, int K,
                             int V, float scale, float eps, float softcap, int gate_kind,
                             void* stream);
+
+/*
+ * Write gates of the memory block (models/qwen/layer.py:71-88; Flash:
+ * models/deepseek/ops/compiled_tensor_ops.py:54-78 after its projections):
+ *   g      [T,H,D] fp32 = -exp(decay_scale_log[h]) * softplus(decay + decay_bias)
+ *   sqrt_b [T,H,D] bf16 = exp(0.5 * logsigmoid(erase))
+ *   beta   [T,H,D] bf16 = sigmoid(write)
+ * decay, erase, write: bf16 rows of H*D channels, `*_stride` elements apart
+ * (views of the projection outputs; stride >= H*D, a multiple of 8);
+ * decay_bias [H*D] bf16, decay_scale_log [H] bf16.  D in {64, 128, 256}.
+ * Inputs and outputs 16-byte aligned.
+ */
+int memt_gdn2_write_gates(const void* decay, int64_t decay_stride, const void* decay_bias,
+                          const void* decay_scale_log, const void* erase, int64_t erase_stride,
+                          const void* write, int64_t write_stride, float* g, void* sqrt_b, void* beta,
+                          int64_t T, int H, int D, void* stream);
+
+/*
+ * The whole prologue of QwenMemoryBlock.packed's commit path
+ * (models/qwen/layer.py:71-97, _write_gates + _symmetric_inputs) in one pass:
+ * g and beta as memt_gdn2_write_gates, and
+ *   q_hat [T,H,D] bf16 = q / sqrt(sum q^2 + eps)                    (l2norm_fwd)
+ *   k_til [T,H,D] bf16 = bf16(sqrt_b * bf16(k / sqrt(sum k^2 + eps)))
+ * q, k: raw bf16 rows with their own strides, as above.  The update then runs
+ * with b = 1 (b = NULL in memt_gdn2_chunk_update), as the reference's
+ * torch.ones_like(sqrt_b) erase does.
+ */
+int memt_gdn2_memory_prologue(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                              const void* decay, int64_t decay_stride, const void* decay_bias,
+                              const void* decay_scale_log, const void* erase, int64_t erase_stride,
+                              const void* write, int64_t write_stride, void* q_hat, void* k_til,
+                              float* g, void* beta, int64_t T, int H, int D, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,41 @@ bool plan_ok(const memt_gdn2_plan* p) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// A bf16 row operand of the prologue: H*D channels per token, rows `stride`
+// elements apart, 16-byte vector loads.
+bool row_operand_ok(const void* p, int64_t stride, int64_t width) {
+  return p != nullptr && aligned16(p) && stride >= width && stride % 8 == 0;
+}
+
+int prologue_common(PrologueArgs& a, const void* decay, int64_t decay_stride, const void* decay_bias,
+                    const void* decay_scale_log, const void* erase, int64_t erase_stride, const void* write,
+                    int64_t write_stride, float* g, void* beta, int64_t T, int H, int D) {
+  if (T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (D != 64 && D != 128 && D != 256) return MEMT_GDN2_EUNSUPPORTED;
+  const int64_t width = (int64_t)H * D;
+  if (T > 0) {
+    if (!row_operand_ok(decay, decay_stride, width) || !row_operand_ok(erase, erase_stride, width) ||
+        !row_operand_ok(write, write_stride, width))
+      return MEMT_GDN2_EINVAL;
+    if (decay_bias == nullptr || decay_scale_log == nullptr || !aligned16(decay_bias)) return MEMT_GDN2_EINVAL;
+    if (g == nullptr || beta == nullptr || !aligned16(g) || !aligned16(beta)) return MEMT_GDN2_EINVAL;
+  }
+  a = PrologueArgs{};
+  a.decay = (const uint16_t*)decay;
+  a.decay_bias = (const uint16_t*)decay_bias;
+  a.decay_scale_log = (const uint16_t*)decay_scale_log;
+  a.erase = (const uint16_t*)erase;
+  a.write = (const uint16_t*)write;
+  a.decay_stride = decay_stride;
+  a.erase_stride = erase_stride;
+  a.write_stride = write_stride;
+  a.g_out = g;
+  a.beta_out = (uint16_t*)beta;
+  a.rows = T * H;
+  a.H = H;
+  return MEMT_GDN2_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -236,6 +271,43 @@ int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void*
   if (gate_kind == MEMT_GDN2_GATE_SOFTCAP_SILU && !(softcap > 0.f)) return MEMT_GDN2_EINVAL;
   return status_of(launch_readout(S, slot_idx, (const __bf16*)q, (const __bf16*)gate, (const __bf16*)weight,
                                   (__bf16*)out, B, H, K, V, scale, eps, softcap, gate_kind, (hipStream_t)stream));
+}
+
+int memt_gdn2_write_gates(const void* decay, int64_t decay_stride, const void* decay_bias,
+                          const void* decay_scale_log, const void* erase, int64_t erase_stride, const void* write,
+                          int64_t write_stride, float* g, void* sqrt_b, void* beta, int64_t T, int H, int D,
+                          void* stream) {
+  PrologueArgs a;
+  const int st = prologue_common(a, decay, decay_stride, decay_bias, decay_scale_log, erase, erase_stride, write,
+                                 write_stride, g, beta, T, H, D);
+  if (st != MEMT_GDN2_OK) return st;
+  if (T > 0 && (sqrt_b == nullptr || !aligned16(sqrt_b))) return MEMT_GDN2_EINVAL;
+  a.erase_out = (uint16_t*)sqrt_b;
+  return status_of(launch_prologue(a, D, false, (hipStream_t)stream));
+}
+
+int memt_gdn2_memory_prologue(const void* q, int64_t q_stride, const void* k, int64_t k_stride, const void* decay,
+                              int64_t decay_stride, const void* decay_bias, const void* decay_scale_log,
+                              const void* erase, int64_t erase_stride, const void* write, int64_t write_stride,
+                              void* q_hat, void* k_til, float* g, void* beta, int64_t T, int H, int D, float eps,
+                              void* stream) {
+  PrologueArgs a;
+  const int st = prologue_common(a, decay, decay_stride, decay_bias, decay_scale_log, erase, erase_stride, write,
+                                 write_stride, g, beta, T, H, D);
+  if (st != MEMT_GDN2_OK) return st;
+  if (T > 0) {
+    const int64_t width = (int64_t)H * D;
+    if (!row_operand_ok(q, q_stride, width) || !row_operand_ok(k, k_stride, width)) return MEMT_GDN2_EINVAL;
+    if (q_hat == nullptr || k_til == nullptr || !aligned16(q_hat) || !aligned16(k_til)) return MEMT_GDN2_EINVAL;
+  }
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.q_stride = q_stride;
+  a.k_stride = k_stride;
+  a.q_out = (uint16_t*)q_hat;
+  a.k_out = (uint16_t*)k_til;
+  a.eps = eps;
+  return status_of(launch_prologue(a, D, true, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -178,7 +178,30 @@ struct StateArgs {
   GroupBuffers grp;    // valid when group_L > 0
 };
 
+// Gate and q/k prologue (models/qwen/layer.py:71-97).  Inputs are bf16 rows
+// of H*D channels with a per-token stride in elements (views of the fused
+// projection outputs); outputs are contiguous [rows = T*H, D].
+struct PrologueArgs {
+  const uint16_t* decay;            // f_down(decay latent) [T, stride]
+  const uint16_t* decay_bias;       // [H*D]
+  const uint16_t* decay_scale_log;  // [H]
+  const uint16_t* erase;            // erase logits [T, stride]
+  const uint16_t* write;            // write logits [T, stride]
+  const uint16_t* q;                // raw q [T, stride] (QK only)
+  const uint16_t* k;                // raw k [T, stride] (QK only)
+  int64_t decay_stride, erase_stride, write_stride, q_stride, k_stride;
+  float* g_out;                     // [T, H, D] fp32
+  uint16_t* beta_out;               // [T, H, D] bf16
+  uint16_t* erase_out;              // [T, H, D] bf16 sqrt(b) (gates only)
+  uint16_t* q_out;                  // [T, H, D] bf16 (QK only)
+  uint16_t* k_out;                  // [T, H, D] bf16 (QK only)
+  int64_t rows;                     // T * H
+  int H;
+  float eps;
+};
+
 // Launchers (return hipError_t of the launch).
+hipError_t launch_prologue(const PrologueArgs& a, int D, bool qk, hipStream_t stream);
 hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bool g_cumulative,
                      bool beta_bf16, hipStream_t stream);
 hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream_t stream);

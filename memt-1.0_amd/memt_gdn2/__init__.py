@@ -27,8 +27,10 @@ from .ops import (
     rms_norm_gated,
     snapshot_read,
     token_memory_packed,
+    memory_prologue,
     token_memory_packed_flash,
     workspace_bytes,
+    write_gates,
 )
 
 RCP_LN2 = 1.4426950216  # FLA/ops/utils/constant.py:10
@@ -58,4 +60,6 @@ __all__ = [
     "token_memory_packed",
     "token_memory_packed_flash",
     "workspace_bytes",
+    "write_gates",
+    "memory_prologue",
 ]

@@ -1,0 +1,95 @@
+"""Memory block of the Nano model on the HIP operators.
+
+``QwenMemoryBlock`` keeps the reference block's parameter names and shapes
+(models/qwen/layer.py:34-69), so a checkpoint's state dict loads unchanged,
+and its ``packed`` entry (models/qwen/layer.py:99-152), the one call the
+serving runtime makes per memory layer.  The dense projections stay torch
+GEMMs (hipBLASLt).  Everything after them runs in this package's kernels:
+
+* query samples: ``l2norm`` -> ``memt_gdn2_read_fwd`` -> ``MemTRMSNormGated``;
+* commit samples: one prologue kernel (gates, ``l2norm(q)``, ``sqrt_b * l2norm(k)``)
+  -> ``token_memory_packed`` -> ``MemTRMSNormGated``.
+"""
+
+from __future__ import annotations
+
+from itertools import accumulate
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .layout import WY_TILE_TOKENS, build_chunk_plan, validate_packed_inputs
+from .norm import MemTRMSNormGated
+from .ops import l2norm, memory_prologue, memt_gdn2_read_fwd, token_memory_packed
+
+
+class QwenMemoryBlock(nn.Module):
+    """``memory_config`` needs ``hidden_size``, ``num_heads``, ``head_dim``,
+    ``chunk_tokens``, ``rms_norm_eps`` and ``output_gate_softcap``."""
+
+    def __init__(self, memory_config, *, device=None):
+        super().__init__()
+        hidden_size = memory_config.hidden_size
+        num_heads = memory_config.num_heads
+        head_dim = memory_config.head_dim
+        self.chunk_tokens = memory_config.chunk_tokens
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.value_dim = num_heads * head_dim
+        self.read_scale = head_dim ** -0.5
+        width = num_heads * head_dim
+        # in_proj rows: q, k, v, erase, write (H*D each), decay latent, output-gate latent (D each)
+        self.qkv_rows = (width,) * 3
+        self.gate_rows = (width, width, head_dim, head_dim)
+        self.qkv_width = 3 * width
+        self.write_gate_rows = self.gate_rows[:-1]
+        self._write_gate_slice = slice(self.qkv_width, self.qkv_width + sum(self.write_gate_rows))
+        self.in_proj = nn.Linear(hidden_size, self.qkv_width + sum(self.gate_rows), bias=False)
+        self.f_down = nn.Linear(head_dim, width, bias=False)
+        self.g_down = nn.Linear(head_dim, width, bias=False)
+        self.decay_scale_log = nn.Parameter(torch.zeros(num_heads))
+        self.decay_bias = nn.Parameter(torch.zeros(width))
+        self.o_norm = MemTRMSNormGated(head_dim, eps=memory_config.rms_norm_eps,
+                                       output_gate_softcap_limit=memory_config.output_gate_softcap)
+        self.to(device=device, dtype=torch.bfloat16)
+        self.eval()
+
+    @torch.no_grad()
+    def packed(self, hidden_states, read_states, *, lengths, commit, write_states):
+        """``(residual [T, H*D] bf16, next_state [N,H,D,D] fp32 | None)``.
+
+        Query samples (``commit=False``) read ``read_states[n]`` for every
+        token of sample ``n``.  Commit samples also scan their tokens from
+        ``write_states[n]``; their read still sees ``read_states[n]``, the
+        state before the commit."""
+        validate_packed_inputs(self, hidden_states, read_states, write_states, lengths)
+        T, H, D = len(hidden_states), self.num_heads, self.head_dim
+        hidden_batch = hidden_states.unsqueeze(0)
+        weight = self.in_proj.weight
+        q, k, v = F.linear(hidden_batch, weight[: self.qkv_width]).split(self.qkv_rows, dim=-1)
+        output_gate = self.g_down(F.linear(hidden_batch, weight[-D:]))
+        if not commit:
+            # host boundaries: the plan is built without a device-to-host copy
+            samples = [0, *accumulate(int(n) for n in lengths)]
+            q_hat = l2norm(q.reshape(1, T, H, D))
+            mask = torch.zeros(len(lengths), dtype=torch.bool)
+            plan = build_chunk_plan(samples, samples, WY_TILE_TOKENS, event_slice=samples, commit_mask=mask)
+            read = memt_gdn2_read_fwd(q_hat, read_states, plan, self.read_scale, out_dtype=v.dtype)
+            output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
+            return output.view(T, self.value_dim), None
+        erase, write, decay_latent = torch.split(
+            F.linear(hidden_batch, weight[self._write_gate_slice]), self.write_gate_rows, dim=-1)
+        decay = self.f_down(decay_latent)
+        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H)
+        read, next_state = token_memory_packed(
+            q_hat, k_til, v.reshape(1, T, H, D), g, beta, read_states, write_states, erase=None, lengths=lengths,
+            scale=self.read_scale, chunk_tokens=self.chunk_tokens)
+        output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
+        return output.view(T, self.value_dim), next_state
+
+    def forward(self, hidden_states, initial_state, *, commit):
+        """Single-request entry (models/qwen/layer.py:154-161)."""
+        return self.packed(hidden_states, initial_state, lengths=[len(hidden_states)], commit=commit,
+                           write_states=initial_state)

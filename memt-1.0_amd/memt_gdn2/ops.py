@@ -30,6 +30,8 @@ __all__ = [
     "rms_norm_gated",
     "readout_fused",
     "workspace_bytes",
+    "write_gates",
+    "memory_prologue",
 ]
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
@@ -400,3 +402,102 @@ def readout_fused(states, q, gate, weight, *, scale: float, eps: float, softcap:
         "readout_fused",
     )
     return out
+
+
+# ---------------------------------------------------------------------------
+# Gate and q/k prologue
+# ---------------------------------------------------------------------------
+
+
+def _rows(x: torch.Tensor, width: int, name: str):
+    """``x`` as ``[T, width]`` bf16 rows with the stride the kernel reads
+    (views of a fused projection keep their row stride; anything else is
+    made contiguous first)."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bf16")
+    if x.shape[-1] != width:
+        raise ValueError(f"{name} must have {width} channels per token, got {tuple(x.shape)}")
+    try:
+        x2 = x.view(-1, width)
+    except RuntimeError:
+        x2 = x.reshape(-1, width).contiguous()
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) < width):
+        x2 = x2.contiguous()
+    return x2, (x2.stride(0) if x2.shape[0] > 1 else width)
+
+
+def _gate_params(decay_bias, decay_scale_log, H: int, D: int, device):
+    bias = decay_bias.reshape(-1)
+    rate = decay_scale_log.reshape(-1)
+    if bias.numel() != H * D or rate.numel() != H:
+        raise ValueError(f"decay_bias must hold {H * D} values and decay_scale_log {H}")
+    bias, rate = (t.to(device=device, dtype=torch.bfloat16).contiguous() for t in (bias, rate))
+    return bias, rate
+
+
+def write_gates(decay, decay_bias, decay_scale_log, erase, write, num_heads: int):
+    """``QwenMemoryBlock._log_decay`` + ``_write_gates`` (models/qwen/layer.py:71-88)
+    from the projection outputs: ``decay`` = f_down(decay latent) [..., T, H*D],
+    ``erase`` and ``write`` logits [..., T, H*D] (bf16 views are read in place).
+    Returns ``(sqrt_b [1,T,H,D] bf16, beta [1,T,H,D] bf16, g [1,T,H,D] fp32)``
+    in the reference's return order (erase, write, log_decay)."""
+    lib = _lib.load()
+    _lib.require_gpu(decay, erase, write)
+    width = decay.shape[-1]
+    if width % num_heads:
+        raise ValueError("decay width must be a multiple of num_heads")
+    D = width // num_heads
+    f2, fs = _rows(decay, width, "decay")
+    e2, es = _rows(erase, width, "erase")
+    w2, ws = _rows(write, width, "write")
+    T = f2.shape[0]
+    if e2.shape[0] != T or w2.shape[0] != T:
+        raise ValueError("decay, erase and write must cover the same tokens")
+    bias, rate = _gate_params(decay_bias, decay_scale_log, num_heads, D, decay.device)
+    g = torch.empty(1, T, num_heads, D, dtype=torch.float32, device=decay.device)
+    sqrt_b = torch.empty(1, T, num_heads, D, dtype=torch.bfloat16, device=decay.device)
+    beta = torch.empty_like(sqrt_b)
+    _lib.check(
+        lib.memt_gdn2_write_gates(f2.data_ptr(), fs, bias.data_ptr(), rate.data_ptr(), e2.data_ptr(), es,
+                                  w2.data_ptr(), ws, g.data_ptr(), sqrt_b.data_ptr(), beta.data_ptr(), T, num_heads,
+                                  D, _lib.stream_of(decay.device)),
+        "write_gates",
+    )
+    return sqrt_b, beta, g
+
+
+def memory_prologue(q, k, decay, decay_bias, decay_scale_log, erase, write, num_heads: int, eps: float = 1e-6):
+    """Commit-path inputs of ``QwenMemoryBlock.packed`` in one kernel
+    (models/qwen/layer.py:71-97): ``q_hat = l2norm(q)``,
+    ``k_til = bf16(sqrt_b * l2norm(k))``, the decay ``g`` and write gate
+    ``beta``.  Raw ``q``/``k`` are [..., T, H*D] bf16 (views of the fused QKV
+    projection are read in place).  Returns ``(q_hat, k_til, beta, g)`` as
+    [1,T,H,D]; the update then runs with the unit erase gate (``erase=None``)."""
+    lib = _lib.load()
+    _lib.require_gpu(q, k, decay, erase, write)
+    width = decay.shape[-1]
+    if width % num_heads:
+        raise ValueError("decay width must be a multiple of num_heads")
+    D = width // num_heads
+    q2, qs = _rows(q, width, "q")
+    k2, ks = _rows(k, width, "k")
+    f2, fs = _rows(decay, width, "decay")
+    e2, es = _rows(erase, width, "erase")
+    w2, ws = _rows(write, width, "write")
+    T = f2.shape[0]
+    if any(x.shape[0] != T for x in (q2, k2, e2, w2)):
+        raise ValueError("q, k, decay, erase and write must cover the same tokens")
+    bias, rate = _gate_params(decay_bias, decay_scale_log, num_heads, D, decay.device)
+    dev = decay.device
+    q_hat = torch.empty(1, T, num_heads, D, dtype=torch.bfloat16, device=dev)
+    k_til = torch.empty_like(q_hat)
+    beta = torch.empty_like(q_hat)
+    g = torch.empty(1, T, num_heads, D, dtype=torch.float32, device=dev)
+    _lib.check(
+        lib.memt_gdn2_memory_prologue(q2.data_ptr(), qs, k2.data_ptr(), ks, f2.data_ptr(), fs, bias.data_ptr(),
+                                      rate.data_ptr(), e2.data_ptr(), es, w2.data_ptr(), ws, q_hat.data_ptr(),
+                                      k_til.data_ptr(), g.data_ptr(), beta.data_ptr(), T, num_heads, D, float(eps),
+                                      _lib.stream_of(dev)),
+        "memory_prologue",
+    )
+    return q_hat, k_til, beta, g

@@ -15,4 +15,4 @@ def bf(a, dev):
 
 def host(t):
     torch.cuda.synchronize()
-    return t.float().cpu().numpy()
+    return t.detach().float().cpu().numpy()
