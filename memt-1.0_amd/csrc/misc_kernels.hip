@@ -77,8 +77,12 @@ __device__ __forceinline__ __bf16 norm_gate_one(float x, float rs, float wt, flo
 // ---------------------------------------------------------------------------
 // Fused decode readout: one workgroup per (sequence, head).
 //   r = bf16(scale * q . S) (fp32 S, fp32 accumulation), then the epilogue.
-// Thread (rg, cg) streams rows [rg*RPT, (rg+1)*RPT) of columns [4cg, 4cg+4)
-// with 16-byte loads; a wave covers contiguous rows of the fp32 state.
+// Thread (rg, cg) streams rows rg, rg + RG, rg + 2RG, ... of columns
+// [4cg, 4cg+4) with 16-byte loads, so one wave instruction reads 64 / CG
+// whole adjacent rows.  Every global load (q, gate, weight and the first NB
+// state rows) is issued before the first wait, and the waits are LDS-only
+// barriers, so the state stream starts at once; with more than NB rows per
+// thread each consumed row is replaced by the next one (a rolling window).
 // ---------------------------------------------------------------------------
 template <int K, int V>
 __global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ S, const int32_t* slot_idx,
@@ -90,8 +94,9 @@ __global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ 
   constexpr int CG = V / 4;          // float4 column groups
   constexpr int RG = 256 / CG;       // row groups
   constexpr int RPT = K / RG;        // rows per thread
-  static_assert(RG * CG == 256 && RPT * RG == K, "readout tiling");
-  __shared__ float q_s[K];
+  constexpr int NB = RPT < 16 ? RPT : 16;  // state rows in flight per thread
+  static_assert(RG * CG == 256 && RPT * RG == K && RPT % NB == 0, "readout tiling");
+  __shared__ float q_s[K > 256 ? K : 256];  // every thread stores: no branch before the first wait
   __shared__ float part[RG][V];
   __shared__ float red[4];
   const int b = blockIdx.x / H, h = blockIdx.x % H;
@@ -99,21 +104,34 @@ __global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ 
   const int slot = slot_idx ? slot_idx[b] : b;
   const float* Sp = S + ((size_t)slot * H + h) * K * V;
   const size_t row = (size_t)b * H + h;
-  if (tid < K) q_s[tid] = (float)q[row * K + tid];
-  __syncthreads();
   const int cg = tid % CG, rg = tid / CG;
-  f32x4 acc = zero4();
-#pragma unroll 8
-  for (int i = 0; i < RPT; ++i) {
-    const int k = rg * RPT + i;
-    const f32x4 s4 = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)k * V + 4 * cg));
-    const float qk = q_s[k];
+  // clamped indices keep these loads unconditional
+  const float qv = (float)q[row * K + (tid < K ? tid : K - 1)];
+  const float gv = (float)gate[row * V + (tid < V ? tid : V - 1)];
+  const float wv = (float)weight[tid < V ? tid : V - 1];
+  asm volatile("" ::: "memory");  // issue q before the state rows: its wait then leaves them in flight
+  f32x4 s4[NB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = fmaf(qk, s4[e], acc[e]);
+  for (int i = 0; i < NB; ++i)
+    s4[i] = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)(i * RG + rg) * V + 4 * cg));
+  q_s[tid] = qv;
+  lds_barrier();
+  f32x4 acc = zero4();
+#pragma unroll
+  for (int j = 0; j < RPT / NB; ++j) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int k = (j * NB + i) * RG + rg;
+      const float qk = q_s[k];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(qk, s4[i][e], acc[e]);
+      if (j + 1 < RPT / NB)
+        s4[i] = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)(k + NB * RG) * V + 4 * cg));
+    }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) part[rg][4 * cg + e] = acc[e];
-  __syncthreads();
+  lds_barrier();
   float r = 0.f, sq = 0.f;
   if (tid < V) {
     float sum = 0.f;
@@ -124,14 +142,13 @@ __global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ 
   }
   sq = wave_sum(sq);
   if ((tid & 63) == 0) red[tid >> 6] = sq;
-  __syncthreads();
+  lds_barrier();
   if (tid < V) {
     float tot = 0.f;
 #pragma unroll
     for (int i = 0; i < (V + 63) / 64; ++i) tot += red[i];
     const float rs = rsqrtf(tot / (float)V + eps);
-    const float g = (float)gate[row * V + tid];
-    out[row * V + tid] = norm_gate_one(r, rs, (float)weight[tid], g, softcap, gate_kind);
+    out[row * V + tid] = norm_gate_one(r, rs, wv, gv, softcap, gate_kind);
   }
 }
 

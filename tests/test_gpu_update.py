@@ -162,3 +162,50 @@ def test_full_size_workload_heads(dev):
     o_ref, h_ref = O.chunked_gdn2(sub["q"], sub["k"], sub["v"], sub["g"], sub["beta"], h0=inp["h0"][:, hs])
     assert O.max_rel_err(ht[:, hs], h_ref) <= TOL
     assert O.parity_err(o[:, :, hs], o_ref, out_bf16=True) <= TOL
+
+
+def _segment_lengths(total, n, seed):
+    """n lengths drawn uniformly from [1024, 32768], rescaled to sum to total
+    (rounded, the last one absorbing the remainder)."""
+    rng = np.random.default_rng(seed)
+    raw = rng.uniform(1024, 32768, n)
+    lengths = [int(round(x)) for x in raw * total / raw.sum()]
+    lengths[-1] = total - sum(lengths[:-1])
+    return lengths
+
+
+def test_varlen_full_size_workload(dev):
+    """4 packed segments summing to 65536 tokens, H=16, d=128, per-segment
+    initial states: two heads of every segment against the fp64 chunked torch
+    oracle, and every head's final state against each segment run alone."""
+    from oracle.gdn2_torch import chunked_gdn2_torch
+
+    T, H, D = 65536, 16, 128
+    lengths = _segment_lengths(T, 4, seed=20261204)
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    print(f"varlen full size lengths={lengths}", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(20261204)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(1, T, H, D, generator=gen, device=dev), dim=-1).to(torch.bfloat16)
+    k = nrm(torch.randn(1, T, H, D, generator=gen, device=dev), dim=-1).to(torch.bfloat16)
+    v = torch.randn(1, T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    g = torch.nn.functional.logsigmoid(torch.randn(1, T, H, D, generator=gen, device=dev))
+    beta = torch.sigmoid(torch.randn(1, T, H, D, generator=gen, device=dev))
+    h0 = torch.randn(4, H, D, D, generator=gen, device=dev) * 0.02
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu, out_mode="causal")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o.float()).all()) and bool(torch.isfinite(ht).all())
+    hs = [3, 12]
+    for n in range(4):
+        a, b = cu[n], cu[n + 1]
+        sl = lambda t: t[0, a:b, hs].double().cpu()  # noqa: E731
+        o_ref, h_ref = chunked_gdn2_torch(sl(q), sl(k), sl(v), sl(g), sl(beta), h0=h0[n, hs].double().cpu(),
+                                          out_mode="causal", dtype=torch.float64)
+        assert O.max_rel_err(host(ht[n, hs]), h_ref.numpy()) <= TOL, n
+        assert O.parity_err(host(o[0, a:b, hs]), o_ref.numpy(), out_bf16=True) <= TOL, n
+        # the segment alone (a different scan grouping): same states within tolerance
+        o1, h1 = memt_gdn2.chunk_gdn2(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
+                                      initial_state=h0[n:n + 1], out_mode="causal")
+        assert O.max_rel_err(host(ht[n]), host(h1[0])) <= TOL, n
