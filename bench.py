@@ -82,12 +82,26 @@ def _inputs(T, H, K, V, seed, dev):
                 g=lg.to(dev), beta=beta.to(dev), h0=h0.to(dev))
 
 
-def bench_update(dev, steps, warmup, T=8192, H=16, D=128, out_mode="causal"):
+def _inputs_on_device(T, H, K, V, seed, dev):
+    """The same distributions as _inputs, drawn on the GPU (the wide-state sets are GBs)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(1, T, H, K, generator=g, device=dev), dim=-1).to(torch.bfloat16)
+    k = nrm(torch.randn(1, T, H, K, generator=g, device=dev), dim=-1).to(torch.bfloat16)
+    v = torch.randn(1, T, H, V, generator=g, device=dev).to(torch.bfloat16)
+    lg = torch.nn.functional.logsigmoid(torch.randn(1, T, H, K, generator=g, device=dev))
+    beta = torch.sigmoid(torch.randn(1, T, H, V, generator=g, device=dev))
+    h0 = torch.randn(1, H, K, V, generator=g, device=dev) * 0.02
+    return dict(q=q, k=k, v=v, g=lg, beta=beta, h0=h0)
+
+
+def bench_update(dev, steps, warmup, T=8192, H=16, D=128, out_mode="causal", on_device=False):
     import memt_gdn2
 
     nbytes_set = update_bytes(T, H, D, D)
     nsets = max(2, int(np.ceil(2 * MALL_BYTES / nbytes_set)))
-    sets = [_inputs(T, H, D, D, seed=20261201 + i, dev=dev) for i in range(nsets)]
+    make = _inputs_on_device if on_device else _inputs
+    sets = [make(T, H, D, D, seed=20261201 + i, dev=dev) for i in range(nsets)]
 
     def step(i):
         s = sets[i % nsets]
@@ -153,6 +167,26 @@ def bench_readout(dev, steps, warmup, B=64, H=16, D=128, gate_kind="softcap_silu
 
 
 COPY_BYTES = 1 << 30  # calibration copy: reads and writes exactly this many bytes
+
+
+def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32):
+    """The wide-state Flash-like shape: chunked update (causal) and a batch-B readout."""
+    steps = min(steps, 20)
+    up = bench_update(dev, steps, warmup, T, H, D, out_mode="causal", on_device=True)
+    ro = bench_readout(dev, steps, warmup, B=B, H=H, D=D)
+    ub, uf = update_bytes(T, H, D, D), update_flops(T, H, D, D, causal=True)
+    t = up["event_ms_mean"] * 1e-3
+    return {
+        "metric": "wide-state GDN-2 update tokens/s @H64 d256 T16K; decode readout GB/s @B32",
+        "value": T / (up["ms_per_step"] * 1e-3), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": up["ms_per_step"], "dtype": "bf16", "data": "synthetic (same distributions, drawn on the GPU)",
+        "config": {"workload": f"chunked GDN-2 update, B=1 H={H} T={T} dk=dv={D} chunk=64, causal output + final state"},
+        "roofline": {"bound": "hbm", "achieved": ub / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ub / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": ub,
+                     "mfma_frac": uf / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, "algorithmic_flops": uf},
+        "readout": {"workload": f"decode readout B={B} H={H} dk=dv={D}", "value": ro["gbs"], "unit": "GB/s",
+                    "us_per_launch": ro["ms_per_launch"] * 1e3, "frac": ro["gbs"] / HBM_PEAK_GBS},
+    }
 
 
 def calibrate(dev, T=8192, H=16, D=128, reps=3):
@@ -236,6 +270,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--mode", default="causal", choices=["causal", "snapshot"])
+    ap.add_argument("--wide", action="store_true",
+                    help="measure the wide-state workload instead (B=1 H=64 T=16384 d=256; batch-32 readout)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the hardware-counter workload (copy of known size, then update steps and readouts)")
     args = ap.parse_args()
@@ -254,6 +290,9 @@ def main():
     T, H, D = 8192, 16, 128
     if args.calibrate:
         calibrate(dev, T, H, D)
+        return
+    if args.wide:
+        print(json.dumps(bench_wide(dev, args.steps, args.warmup)))
         return
 
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)

@@ -7,7 +7,7 @@ using namespace memt;
 
 namespace {
 
-bool supported_kv(int K, int V) { return (K == 64 && V == 64) || (K == 128 && V == 128); }
+bool supported_kv(int K, int V) { return K == V && (K == 64 || K == 128 || K == 256); }
 
 int status_of(hipError_t e) { return e == hipSuccess ? MEMT_GDN2_OK : MEMT_GDN2_ELAUNCH; }
 

@@ -379,6 +379,9 @@ hipError_t launch_wy_export(const WyBuffers& in, const int32_t* chunk_tok0, cons
   else if (K == 128 && V == 128)
     hipLaunchKernelGGL((wy_export_kernel<128, 128>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
                        Aqk, qg);
+  else if (K == 256 && V == 256)
+    hipLaunchKernelGGL((wy_export_kernel<256, 256>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
+                       Aqk, qg);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -394,6 +397,9 @@ hipError_t launch_wy_import(const __bf16* w, const __bf16* u, const __bf16* kg, 
                        out);
   else if (K == 128 && V == 128)
     hipLaunchKernelGGL((wy_import_kernel<128, 128>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
+                       out);
+  else if (K == 256 && V == 256)
+    hipLaunchKernelGGL((wy_import_kernel<256, 256>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
                        out);
   else
     return hipErrorInvalidValue;

@@ -1,8 +1,9 @@
 // Inter-chunk state scan of the chunked GDN-2 update.
 //
-// One workgroup (8 waves) per (sequence or chunk group, head) holds the head's
-// whole K x NC fp32 state in MFMA accumulators and walks the chunks in order
-// (models/qwen/ops/_triton/state.py:76-115):
+// One workgroup (8 waves) per (sequence or chunk group, head, column slice)
+// holds a K x NC slice of the head's fp32 state in MFMA accumulators (all V
+// columns up to d = 128, 64-column slices at d = 256) and walks the chunks in
+// order (models/qwen/ops/_triton/state.py:76-115):
 //
 //   snapshot S if the chunk starts a read block
 //   V_new = U - W . f16(S)                         (erase path)
@@ -116,11 +117,13 @@ __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int 
   count = (soff[n + 1] - soff[n] + L - 1) / L;
 }
 
-// MODE 0: the scan (per sequence, or per group from its start state), NC = V
-// MODE 1: group transition P_g, columns of the K x K identity, no values, NC = K
-// MODE 2: group contribution Q_g, value columns from a zero state, NC = V
+// MODE 0: the scan (per sequence, or per group from its start state), columns of S
+// MODE 1: group transition P_g, columns of the K x K identity, no values
+// MODE 2: group contribution Q_g, value columns from a zero state
+// The workgroup carries NC columns starting at column cbase; its LDS tiles
+// hold only those columns.
 template <int K, int V, int NC, bool CAUSAL, int MODE>
-__device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, _Float16* S_lds,
+__device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, int cbase, _Float16* S_lds,
                                           _Float16* Vn_lds) {
   using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
@@ -153,7 +156,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = w & 3, half = w >> 2;
   const int lr = lane & 15, lg = lane >> 4;
-  const int col0 = half * (NC / 2);  // first state column of this wave
+  const int lcol0 = half * (NC / 2);  // first column of this wave in the LDS tiles
+  const int col0 = cbase + lcol0;     // and in the state
 
   // S tile (rt, ct): rows 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr
   f32x4 S[RT][CT];
@@ -192,7 +196,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         f16x4 b4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) b4[e] = (_Float16)S[rt][ct][e];
-        *(f16x4*)(&S_lds[(col0 + 16 * ct + lr) * SKP + 16 * (q * RT + rt) + 4 * lg]) = b4;
+        *(f16x4*)(&S_lds[(lcol0 + 16 * ct + lr) * SKP + 16 * (q * RT + rt) + 4 * lg]) = b4;
       }
   };
 
@@ -304,7 +308,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       for (int s = 0; s < KS; ++s) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-          const f16x8 sb = b_operand(S_lds, SKP, col0 + 16 * ct + lr, s);
+          const f16x8 sb = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s);
           acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
           if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
         }
@@ -320,7 +324,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         f16x4 vn;
 #pragma unroll
         for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)un[ct][e] - acc[ct][e]);
-        *(f16x4*)(&Vn_lds[(col0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
+        *(f16x4*)(&Vn_lds[(lcol0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
       }
       lds_barrier();
 
@@ -329,7 +333,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) vb[ct][s] = b_operand(Vn_lds, VNP, col0 + 16 * ct + lr, s);
+        for (int s = 0; s < 2; ++s) vb[ct][s] = b_operand(Vn_lds, VNP, lcol0 + 16 * ct + lr, s);
       if (cur_flags & MEMT_GDN2_CHUNK_COMMIT) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -407,24 +411,33 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   }
 }
 
+// Blocks are (slice, unit, head) with the slice outermost: with units * H a
+// multiple of 8 the slices of one (unit, head), which read the same chunk
+// records, land on the same XCD (blocks go to XCDs round-robin).
 template <int K, int V, bool CAUSAL>
-__global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 S_lds[V * (K + kSPad)];
-  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[V * (kChunk + kVPad)];
-  scan_body<K, V, V, CAUSAL, 0>(a, blockIdx.x / a.H, blockIdx.x % a.H, S_lds, Vn_lds);
+__global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a, int units) {
+  constexpr int NS = scan_slice(V);
+  __shared__ __attribute__((aligned(16))) _Float16 S_lds[NS * (K + kSPad)];
+  __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NS * (kChunk + kVPad)];
+  const int per = units * a.H, b = blockIdx.x % per;
+  scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds);
 }
 
-// Phase 1 of the two-level scan: blocks [0, units H) form P_g, the rest Q_g.
+// Phase 1 of the two-level scan: the first (K / slice) units H blocks form
+// P_g, the rest Q_g.
 template <int K, int V>
 __global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int units) {
-  constexpr int NCM = K > V ? K : V;
+  constexpr int NSK = scan_slice(K), NSV = scan_slice(V);
+  constexpr int NCM = NSK > NSV ? NSK : NSV;
   __shared__ __attribute__((aligned(16))) _Float16 S_lds[NCM * (K + kSPad)];
   __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NCM * (kChunk + kVPad)];
-  const int b = blockIdx.x, per = units * a.H;
-  if (b < per)
-    scan_body<K, V, K, false, 1>(a, b / a.H, b % a.H, S_lds, Vn_lds);
+  const int per = units * a.H, nP = per * (K / NSK);
+  const int b = blockIdx.x < nP ? blockIdx.x : blockIdx.x - nP;
+  const int r = b % per, slice = b / per;
+  if (blockIdx.x < nP)
+    scan_body<K, V, NSK, false, 1>(a, r / a.H, r % a.H, NSK * slice, S_lds, Vn_lds);
   else
-    scan_body<K, V, V, false, 2>(a, (b - per) / a.H, (b - per) % a.H, S_lds, Vn_lds);
+    scan_body<K, V, NSV, false, 2>(a, r / a.H, r % a.H, NSV * slice, S_lds, Vn_lds);
 }
 
 // Phase 2 of the two-level scan, one workgroup per (sequence, head, 32 state
@@ -567,14 +580,15 @@ hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
   int units = a.n_seq;
   if (a.group_L > 0) {
     units = group_bound(a.n_chunk, a.n_seq, a.group_L);
-    hipLaunchKernelGGL((trans_kernel<K, V>), dim3(2 * units * a.H), dim3(kScanThreads), 0, stream, a, units);
+    const int nt = units * a.H * (K / scan_slice(K) + V / scan_slice(V));
+    hipLaunchKernelGGL((trans_kernel<K, V>), dim3(nt), dim3(kScanThreads), 0, stream, a, units);
     hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), dim3(256), 0, stream, a);
   }
-  const dim3 grid(units * a.H), block(kScanThreads);
+  const dim3 grid(units * a.H * (V / scan_slice(V))), block(kScanThreads);
   if (causal)
-    hipLaunchKernelGGL((state_kernel<K, V, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, true>), grid, block, 0, stream, a, units);
   else
-    hipLaunchKernelGGL((state_kernel<K, V, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((state_kernel<K, V, false>), grid, block, 0, stream, a, units);
   return hipGetLastError();
 }
 
@@ -584,6 +598,7 @@ hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream
   if (a.n_seq == 0) return hipSuccess;
   if (K == 64 && V == 64) return launch_t<64, 64>(a, causal, stream);
   if (K == 128 && V == 128) return launch_t<128, 128>(a, causal, stream);
+  if (K == 256 && V == 256) return launch_t<256, 256>(a, causal, stream);
   return hipErrorInvalidValue;
 }
 

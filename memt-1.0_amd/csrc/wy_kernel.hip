@@ -35,7 +35,8 @@
 //             exact identity-matrix MFMA transpose of each wave's rows.
 // Precision: every MFMA operand of the state scan (W, b k 2^gk, qg, beta v, A, U,
 // kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.
-// LDS stays under 80 KB at d = 128, so two workgroups share a CU.
+// LDS stays under 80 KB at d = 128, so two workgroups share a CU; d = 256 takes
+// 130 KB and one workgroup per CU.
 #include "gdn2_internal.h"
 
 namespace memt {
@@ -50,7 +51,7 @@ __device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
 }
 
 template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT>
-__global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
+__global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   constexpr int C = kChunk;
   constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;
   constexpr int XP = C + 8;   // element pitch of the column-major xw / xu tiles
@@ -193,10 +194,10 @@ __global__ __launch_bounds__(256, 2) void wy_kernel(WyArgs a) {
         for (int e = 0; e < 4; ++e) gk[s][4 * half + e] = lv[e];
       }
     }
-  if (tid < 2 * K) {
+  for (int idx = tid; idx < 2 * K; idx += 256) {
     // two threads per channel: part 0 writes the block starts, their ratios and gk_last,
     // part 1 the powers used by kg and by xw / qg
-    const int c = tid % K, part = tid / K;
+    const int c = idx % K, part = idx / K;
     float ref[4], last;
     if constexpr (!G_CUM) {
       // same summation order as the per-lane offsets above, so fa == 1 exactly at block starts
@@ -560,6 +561,7 @@ hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bo
   if (n_chunk == 0) return hipSuccess;
   if (K == 64 && V == 64) return launch_kv<64, 64>(a, n_chunk, causal, g_cumulative, beta_bf16, stream);
   if (K == 128 && V == 128) return launch_kv<128, 128>(a, n_chunk, causal, g_cumulative, beta_bf16, stream);
+  if (K == 256 && V == 256) return launch_kv<256, 256>(a, n_chunk, causal, g_cumulative, beta_bf16, stream);
   return hipErrorInvalidValue;
 }
 
