@@ -24,8 +24,8 @@
 // one token and stores 8 bytes.
 //
 // Prefetch: each record fragment of chunk c + 1 is loaded right after its last
-// use in chunk c (one register buffer); plan entries come from a per-wave
-// cache of 64 chunks.  Loads past the last chunk reload the last chunk, so
+// use in chunk c (one register buffer), between the MFMAs that consume the
+// other fragments; plan entries come from a per-wave cache of 64 chunks.  Loads past the last chunk reload the last chunk, so
 // every load is unconditional and the compiler's vmcnt waits stay exact.
 //
 // Long sequences use a two-level scan over groups of chunks (the recurrence is
@@ -228,40 +228,56 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   };
 
   F f;
-  // fragments used by the V_new / qg . S products
-  auto load_a = [&](int c) {
-    const size_t unit = (size_t)c * H + h;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const size_t fo = unit * (size_t)(C * K) + ((size_t)(q * KS + s) * 64 + lane) * 8;
-      f.w[s] = *(const f16x8*)(a.in.W + fo);
-      if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + fo);
-    }
+  // Record fragments, each (re)loaded right after its last use: the loads of
+  // chunk c + 1 spread over chunk c's MFMAs instead of queueing in bursts.
+  auto load_w = [&](int c, int s) {
+    const size_t fo = ((size_t)c * H + h) * (size_t)(C * K) + ((size_t)(q * KS + s) * 64 + lane) * 8;
+    f.w[s] = *(const f16x8*)(a.in.W + fo);
+    if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + fo);
+  };
+  auto load_u = [&](int c) {
     if constexpr (MODE != 1) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
-        f.u[ct] = *(const f16x4*)(a.in.U + unit * (size_t)(C * V) +
+        f.u[ct] = *(const f16x4*)(a.in.U + ((size_t)c * H + h) * (size_t)(C * V) +
                                   ((size_t)(q * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
     } else {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) f.u[ct] = f16x4{};
     }
   };
-  // fragments used by the state update and the causal output
-  auto load_b = [&](int c) {
-    const size_t unit = (size_t)c * H + h;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int rtile = q * RT + rt;
-      f.d[rt] = *(const f32x4*)(a.in.decay + unit * K + 16 * rtile + 4 * lg);
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        f.kg[rt][s] = *(const f16x8*)(a.in.kgT + unit * (size_t)(C * K) + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
-    }
+  auto load_aq = [&](int c) {
     if constexpr (CAUSAL) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        f.aq[s] = *(const f16x8*)(a.in.Aqk + unit * (size_t)(C * C) + ((size_t)(q * 2 + s) * 64 + lane) * 8);
+        f.aq[s] = *(const f16x8*)(a.in.Aqk + ((size_t)c * H + h) * (size_t)(C * C) +
+                                  ((size_t)(q * 2 + s) * 64 + lane) * 8);
+    }
+  };
+  auto load_kd = [&](int c, int rt) {
+    const size_t unit = (size_t)c * H + h;
+    const int rtile = q * RT + rt;
+    f.d[rt] = *(const f32x4*)(a.in.decay + unit * K + 16 * rtile + 4 * lg);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      f.kg[rt][s] = *(const f16x8*)(a.in.kgT + unit * (size_t)(C * K) + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
+  };
+  // the first chunk's fragments, in the order the loop consumes and reloads them,
+  // so that its vmcnt waits stay partial from the first iteration on
+  auto load_all = [&](int c) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      load_w(c, s);
+      asm volatile("" ::: "memory");
+    }
+    load_u(c);
+    asm volatile("" ::: "memory");
+    load_aq(c);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      load_kd(c, rt);
+      asm volatile("" ::: "memory");
     }
   };
 
@@ -279,8 +295,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   if (c_begin < c_end) {
     const int c_last = c_end - 1;
     meta(c_begin);
-    load_a(c_begin);
-    load_b(c_begin);
+    load_all(c_begin);
     for (int c = c_begin; c < c_end; ++c) {
       const int cn = min(c + 1, c_last);
       if constexpr (MODE == 0) {
@@ -297,6 +312,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
               }
         }
       }
+      const int cur_flags = flags, cur_tok0 = tok0, cur_len = len;
+      meta(cn);
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
 #pragma unroll
@@ -312,13 +329,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
           acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
           if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
         }
+        load_w(cn, s);  // W and qg of the next chunk, step s
       }
       f16x4 un[CT];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) un[ct] = f.u[ct];
-      const int cur_flags = flags, cur_tok0 = tok0, cur_len = len;
-      meta(cn);
-      load_a(cn);  // W, qg and U of the next chunk
+      load_u(cn);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         f16x4 vn;
@@ -328,24 +344,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       }
       lds_barrier();
 
-      // ---- S = decay * S + kg^T . V_new; causal output ----
+      // ---- causal output; S = decay * S + kg^T . V_new ----
       f16x8 vb[CT][2];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int s = 0; s < 2; ++s) vb[ct][s] = b_operand(Vn_lds, VNP, lcol0 + 16 * ct + lr, s);
-      if (cur_flags & MEMT_GDN2_CHUNK_COMMIT) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
-          }
-        }
-      }
       if constexpr (CAUSAL) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
@@ -354,8 +358,22 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
           for (int s = 0; s < 2; ++s) acco[ct] = mfma_f16(vb[ct][s], f.aq[s], acco[ct]);
         }
+        load_aq(cn);
       }
-      load_b(cn);  // decay, kg^T and Aqk of the next chunk
+      const bool commit = (cur_flags & MEMT_GDN2_CHUNK_COMMIT) != 0;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        if (commit) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
+          }
+        }
+        load_kd(cn, rt);  // decay and kg^T rows of the next chunk
+      }
       if constexpr (CAUSAL) {
         // lane holds o[16 q + lr][col0 + 16 ct + 4 lg + e]
         const int t = 16 * q + lr;

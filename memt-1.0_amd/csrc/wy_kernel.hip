@@ -37,6 +37,8 @@
 // kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.
 // LDS stays under 80 KB at d = 128, so two workgroups share a CU; d = 256 takes
 // 130 KB and one workgroup per CU.
+#include <type_traits>
+
 #include "gdn2_internal.h"
 
 namespace memt {
@@ -84,88 +86,62 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   const size_t rowV = ((size_t)(tok0 + (valid ? t : 0)) * H + h) * V;
 
   // ---- loads: every per-token input of this lane's row, in slot order ----
+  // Issued in the order of first use (g for the cumsum, then v and beta, then
+  // k / b / q for the per-channel loop), so each phase waits only for its own
+  // inputs and the cumsum and factor phases run while the rest is in flight.
+  // Rows past the chunk end read row 0 of the chunk and are zeroed where used.
   bf16x8 kraw[KS], braw[HAS_B ? KS : 1], qraw[CAUSAL ? KS : 1];
   float g[KS][8];
-  f16x8 xu8[VS];
+  using BetaRaw = typename std::conditional<sizeof(BetaT) == 4, f32x4, bf16x4>::type;
+  bf16x4 vraw[VS][2];
+  BetaRaw btraw[VS][2];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const f32x4 gg = *(const f32x4*)(a.g + rowK + 32 * s + 16 * half + 4 * lg);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g[s][4 * half + e] = gg[e];
+    }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < VS; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int c0 = 32 * s + 16 * half + 4 * lg;
-      // rows past the chunk end read row 0 of the chunk and are zeroed below
-      bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
+      vraw[s][half] = *(const bf16x4*)(a.v + rowV + c0);
+      btraw[s][half] = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+    }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
       bf16x4 bb{}, qq{};
       if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
       if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
-      f32x4 gg = *(const f32x4*)(a.g + rowK + c0);
-      if (!valid) {
-        kk = bf16x4{};
-        bb = bf16x4{};
-        qq = bf16x4{};
-        gg = zero4();
-      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         kraw[s][4 * half + e] = kk[e];
         if constexpr (HAS_B) braw[s][4 * half + e] = bb[e];
         if constexpr (CAUSAL) qraw[s][4 * half + e] = qq[e];
-        g[s][4 * half + e] = gg[e];
       }
     }
-  }
   auto kf = [&](int s, int j) { return (float)kraw[s][j]; };
   auto bkf = [&](int s, int j) { return HAS_B ? (float)kraw[s][j] * (float)braw[s][j] : (float)kraw[s][j]; };
   auto qf = [&](int s, int j) { return CAUSAL ? (float)qraw[s][j] : 0.f; };
-#pragma unroll
-  for (int s = 0; s < VS; ++s) {
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
-      bf16x4 vv = *(const bf16x4*)(a.v + rowV + c0);
-      f32x4 bt;
-      if constexpr (sizeof(BetaT) == 4) {
-        bt = *(const f32x4*)((const float*)a.beta + rowV + c0);
-      } else {
-        const bf16x4 b4 = *(const bf16x4*)((const __bf16*)a.beta + rowV + c0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bt[e] = (float)b4[e];
-      }
-      if (!valid) {
-        vv = bf16x4{};
-        bt = zero4();
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xu8[s][4 * half + e] = (_Float16)((float)vv[e] * bt[e]);
-    }
-  }
-
-  // Identity-matrix selectors: element j of lane (lr, lg) is 1 where the slot's channel
-  // is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
-  // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
-  f16x8 sel_h[2];
-#pragma unroll
-  for (int half = 0; half < 2; ++half)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const bool one = (j >> 2) == half && 4 * lg + (j & 3) == lr;
-      sel_h[half][j] = (_Float16)(one ? 1.f : 0.f);
-    }
-  // beta v to LDS now, column-major (channel rows, token columns)
-#pragma unroll
-  for (int ct = 0; ct < VT; ++ct) {
-    const f32x4 tr = mfma_f16(xu8[ct >> 1], sel_h[ct & 1], zero4());
-    f16x4 o4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
-    *(f16x4*)(&xu_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
-  }
 
   // ---- cumsum: inclusive within the 16-token block, then block offsets ----
   float gk[KS][8];
 #pragma unroll
   for (int s = 0; s < KS; ++s)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) gk[s][j] = G_CUM ? g[s][j] : row_inclusive_scan(g[s][j]);
+    for (int j = 0; j < 8; ++j) {
+      g[s][j] = valid ? g[s][j] : 0.f;
+      gk[s][j] = G_CUM ? g[s][j] : row_inclusive_scan(g[s][j]);
+    }
 #pragma unroll
   for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -230,6 +206,45 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     }
   }
   lds_barrier();
+
+  // Identity-matrix selectors: element j of lane (lr, lg) is 1 where the slot's channel
+  // is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
+  // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
+  f16x8 sel_h[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool one = (j >> 2) == half && 4 * lg + (j & 3) == lr;
+      sel_h[half][j] = (_Float16)(one ? 1.f : 0.f);
+    }
+  // beta v to LDS, column-major (channel rows, token columns); read by the U product
+#pragma unroll
+  for (int s = 0; s < VS; ++s) {
+    f16x8 xu8;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * (float)btraw[s][half][e] : 0.f);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int ct = 2 * s + half;
+      const f32x4 tr = mfma_f16(xu8, sel_h[half], zero4());
+      f16x4 o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
+      *(f16x4*)(&xu_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
+    }
+  }
+  if (!valid) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      kraw[s] = bf16x8{};
+      if constexpr (HAS_B) braw[s] = bf16x8{};
+      if constexpr (CAUSAL) qraw[s] = bf16x8{};
+    }
+  }
 
   // ---- in-block decay span: a wide block takes exact diagonal products ----
   float span = 0.f;
