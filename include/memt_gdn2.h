@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 3
+#define MEMT_GDN2_ABI_VERSION 4
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -64,6 +64,28 @@ typedef struct memt_gdn2_plan {
   int32_t n_block; /* rows of `snaps` */
   int32_t reserved;
 } memt_gdn2_plan;
+
+/*
+ * Host-side chunk plan (no device work, no allocation, no device-to-host copy).
+ * Replaces the reference's ChunkPlan builder (models/qwen/ops/layout.py:47-135),
+ * which copies its device boundary tensors to the host on every call.
+ * Boundaries are host int32 arrays: read [n_read], sample [n_sample] and event
+ * [n_event], each non-decreasing from 0 to the same token total.  Every event
+ * is cut into chunks of at most wy_tile_tokens (1..64) tokens.
+ * memt_gdn2_plan_count writes the chunk count; memt_gdn2_plan_build fills
+ * caller-owned host tables of that size: chunk_tok0, chunk_len,
+ * chunk_block_ids (the read block of each chunk's first token), chunk_flags
+ * (MEMT_GDN2_CHUNK_*), sample_chunk_offsets [n_sample] and, when not NULL,
+ * chunk_indices [2 n_chunk] (event, chunk within event), chunk_is_block_start,
+ * chunk_commits.  commit_mask [n_event - 1] may be NULL (every event commits).
+ */
+int memt_gdn2_plan_count(const int32_t* event, int n_event, int wy_tile_tokens, int32_t* n_chunk);
+int memt_gdn2_plan_build(const int32_t* read, int n_read, const int32_t* sample, int n_sample,
+                         const int32_t* event, int n_event, const uint8_t* commit_mask,
+                         int wy_tile_tokens, int32_t n_chunk, int32_t* chunk_tok0,
+                         int32_t* chunk_len, int32_t* sample_chunk_offsets,
+                         int32_t* chunk_block_ids, int32_t* chunk_flags, int32_t* chunk_indices,
+                         int32_t* chunk_is_block_start, int32_t* chunk_commits);
 
 int memt_gdn2_abi_version(void);
 const char* memt_gdn2_strerror(int status);

@@ -21,7 +21,7 @@ BUILD_DIR = ROOT / "_build"
 LIB_NAME = "libmemt_gdn2.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["abi.hip", "wy_kernel.hip", "state_kernel.hip", "misc_kernels.hip", "prologue_kernel.hip"]
+SOURCES = ["abi.hip", "wy_kernel.hip", "state_kernel.hip", "misc_kernels.hip", "prologue_kernel.hip", "plan.cpp"]
 
 # -packed-fp32-ops off: hipcc must not emit packed fp32 VALU ops for this code.
 HIPCC_FLAGS = [

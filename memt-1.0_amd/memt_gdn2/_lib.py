@@ -33,7 +33,7 @@ OUT_CAUSAL = 2
 CHUNK_BLOCK_START = 1
 CHUNK_COMMIT = 2
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class Plan(ctypes.Structure):
@@ -78,6 +78,8 @@ _SIGNATURES = {
     "memt_gdn2_read_fwd": (_I, [_P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _P]),
     "memt_gdn2_rms_norm_gated": (_I, [_P, _P, _P, _P, _I64, _I, _F, _F, _I, _P]),
     "memt_gdn2_readout_fused": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _I, _P]),
+    "memt_gdn2_plan_count": (_I, [_P, _I, _I, _P]),
+    "memt_gdn2_plan_build": (_I, [_P, _I, _P, _I, _P, _I, _P, _I, ctypes.c_int32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "memt_gdn2_write_gates": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I, _I, _P]),
     "memt_gdn2_memory_prologue": (
         _I,

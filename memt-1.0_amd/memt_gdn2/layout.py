@@ -3,12 +3,14 @@
 Mirrors the reference's plan types and builders
 (models/qwen/ops/layout.py:18-135, models/qwen/ops/packed.py:16-31,
 models/common/packed.py:8-34).  Plans are computed on the host from integer
-boundaries and uploaded with one host-to-device copy; when the caller hands
-in host integers (``lengths``) nothing is copied back from the device.
+boundaries by the library's C++ plan builder and uploaded with one
+host-to-device copy; when the caller hands in host integers (``lengths``)
+nothing is copied back from the device.
 """
 
 from __future__ import annotations
 
+import ctypes
 from collections import OrderedDict
 from dataclasses import dataclass
 from itertools import accumulate
@@ -80,8 +82,15 @@ def _host_ints(x) -> np.ndarray:
     return np.asarray(x, dtype=np.int64).reshape(-1)
 
 
+def _i32(x: np.ndarray) -> np.ndarray:
+    if np.any(x < 0) or np.any(x > np.iinfo(np.int32).max):
+        raise ValueError("token boundaries must fit int32")
+    return np.ascontiguousarray(x, dtype=np.int32)
+
+
 def _host_plan(read, sample, wy, event, commit_mask):
-    """Integer chunk table (numpy int64) of a set of boundaries."""
+    """Integer chunk table of a set of boundaries, built by the library's host
+    plan builder (memt_gdn2_plan_count / memt_gdn2_plan_build)."""
     if wy <= 0 or wy > WY_TILE_TOKENS:
         raise ValueError(f"wy_tile_tokens must be in 1..{WY_TILE_TOKENS}")
     if len(event) < 1 or event[0] != 0 or np.any(np.diff(event) < 0):
@@ -89,41 +98,32 @@ def _host_plan(read, sample, wy, event, commit_mask):
     for name, arr in (("read", read), ("sample", sample)):
         if len(arr) < 1 or arr[0] != 0 or arr[-1] != event[-1] or np.any(np.diff(arr) < 0):
             raise ValueError(f"{name} boundaries must span the event tokens")
-    ev_len = np.diff(event)
-    per_event = (ev_len + wy - 1) // wy
-    event_first = np.concatenate(([0], np.cumsum(per_event)))
-    num_chunk = int(event_first[-1])
-    chunk_event = np.repeat(np.arange(len(ev_len), dtype=np.int64), per_event)
-    chunk_sub = np.arange(num_chunk, dtype=np.int64) - event_first[chunk_event]
-    tok0 = event[chunk_event] + chunk_sub * wy
-    clen = np.minimum(event[chunk_event + 1] - tok0, wy)
-    sample_offsets = event_first[np.searchsorted(event, sample, side="left")]
-    block_ids = np.searchsorted(read, tok0, side="right") - 1
-    block_start = tok0 == read[block_ids]
-    if commit_mask is None:
-        commits = np.ones(num_chunk, dtype=bool)
-    else:
-        cm = _host_ints(commit_mask).astype(bool)
-        if len(cm) != len(ev_len):
+    n_event = len(event) - 1
+    cm = None
+    if commit_mask is not None:
+        cm = np.ascontiguousarray(_host_ints(commit_mask).astype(bool), dtype=np.uint8)
+        if len(cm) != n_event:
             raise ValueError("commit_mask needs one entry per write event")
-        commits = cm[chunk_event]
-    return dict(
-        num_event=len(ev_len),
-        num_block=len(read) - 1,
-        num_sample=len(sample) - 1,
-        num_chunk=num_chunk,
-        total_tokens=int(event[-1]),
-        event_slice=event,
-        chunk_indices=np.stack((chunk_event, chunk_sub), axis=-1).reshape(-1),
-        sample_chunk_offsets=sample_offsets,
-        chunk_block_ids=block_ids,
-        chunk_is_block_start=block_start.astype(np.int64),
-        chunk_tok0=tok0,
-        chunk_len=clen,
-        chunk_commits=commits.astype(np.int64),
-        chunk_flags=(block_start.astype(np.int64) * _lib.CHUNK_BLOCK_START
-                     + commits.astype(np.int64) * _lib.CHUNK_COMMIT),
+    read, sample, event = _i32(read), _i32(sample), _i32(event)
+    lib = _lib.load()
+    n = ctypes.c_int32(0)
+    _lib.check(lib.memt_gdn2_plan_count(event.ctypes.data, len(event), wy, ctypes.byref(n)), "build_chunk_plan")
+    nc = n.value
+    out = {name: np.zeros(nc, np.int32) for name in
+           ("chunk_tok0", "chunk_len", "chunk_block_ids", "chunk_flags", "chunk_is_block_start", "chunk_commits")}
+    out["chunk_indices"] = np.zeros(2 * nc, np.int32)
+    out["sample_chunk_offsets"] = np.zeros(len(sample), np.int32)
+    ptrs = {k: v.ctypes.data for k, v in out.items()}
+    _lib.check(
+        lib.memt_gdn2_plan_build(read.ctypes.data, len(read), sample.ctypes.data, len(sample), event.ctypes.data,
+                                 len(event), None if cm is None else cm.ctypes.data, wy, nc, ptrs["chunk_tok0"],
+                                 ptrs["chunk_len"], ptrs["sample_chunk_offsets"], ptrs["chunk_block_ids"],
+                                 ptrs["chunk_flags"], ptrs["chunk_indices"], ptrs["chunk_is_block_start"],
+                                 ptrs["chunk_commits"]),
+        "build_chunk_plan",
     )
+    return dict(num_event=n_event, num_block=len(read) - 1, num_sample=len(sample) - 1, num_chunk=nc,
+                total_tokens=int(event[-1]), event_slice=event, **out)
 
 
 _FIELDS = (

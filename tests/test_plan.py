@@ -1,6 +1,8 @@
 """Chunk plans (models/qwen/ops/layout.py:47-135, models/qwen/ops/packed.py:16-31):
-hand-counted tables, and the product's vectorised builder against the
-oracle's loop restatement.  CPU only."""
+hand-counted tables, and the library's C++ plan builder against the
+oracle's loop restatement.  CPU only (the builder is host code)."""
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -8,6 +10,7 @@ import torch
 
 from oracle import gdn2 as O
 
+from memt_gdn2 import _lib
 from memt_gdn2 import layout as L
 
 
@@ -85,3 +88,51 @@ def test_boundaries_and_validation():
     s = torch.zeros(1, 2, 4, 4)
     with pytest.raises(ValueError, match="CUDA BF16"):
         L.validate_packed_inputs(Block, h, s, s, [5])  # a CPU tensor is rejected like the reference
+
+
+def _sorted_bounds(rng, total, n):
+    """n - 1 interior boundaries in [0, total], repeats allowed (empty blocks / events)."""
+    inner = np.sort(rng.integers(0, total + 1, n - 1)) if n > 1 else np.zeros(0, np.int64)
+    return [0, *inner.tolist(), total]
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_builder_matches_oracle_on_independent_boundaries(seed):
+    """Read, sample and event boundaries drawn independently (empty read blocks,
+    empty events, samples that start mid-event), every WY tile size."""
+    rng = np.random.default_rng(100 + seed)
+    total = int(rng.integers(0, 700))
+    read = _sorted_bounds(rng, total, int(rng.integers(1, 6)))
+    sample = _sorted_bounds(rng, total, int(rng.integers(1, 6)))
+    event = _sorted_bounds(rng, total, int(rng.integers(1, 9)))
+    wy = int(rng.choice([1, 7, 16, 33, 64]))
+    cm = [int(x) for x in rng.integers(0, 2, len(event) - 1)] if seed % 2 else None
+    plan = L.build_chunk_plan(read, sample, wy, event_slice=event, commit_mask=cm, device="cpu")
+    ref = O.build_chunk_plan(read, sample, wy, event_slice=event, commit_mask=cm)
+    for name in ("event_slice", "chunk_tok0", "chunk_len", "sample_chunk_offsets", "chunk_block_ids",
+                 "chunk_is_block_start", "chunk_commits"):
+        assert np.array_equal(_host(plan, name), getattr(ref, name)), name
+    assert np.array_equal(_host(plan, "chunk_indices").reshape(-1, 2), ref.chunk_indices.reshape(-1, 2))
+    flags = ref.chunk_is_block_start * _lib.CHUNK_BLOCK_START + ref.chunk_commits * _lib.CHUNK_COMMIT
+    assert np.array_equal(_host(plan, "chunk_flags"), flags)
+
+
+def test_builder_c_abi_rejects_bad_boundaries():
+    lib = _lib.load()
+    i32 = lambda xs: (ctypes.c_int32 * len(xs))(*xs)  # noqa: E731
+    n = ctypes.c_int32(-1)
+    assert lib.memt_gdn2_plan_count(i32([0, 10, 5]), 3, 64, ctypes.byref(n)) == _lib.EINVAL  # decreasing
+    assert lib.memt_gdn2_plan_count(i32([1, 10]), 2, 64, ctypes.byref(n)) == _lib.EINVAL  # not from 0
+    assert lib.memt_gdn2_plan_count(i32([0, 10]), 2, 65, ctypes.byref(n)) == _lib.EINVAL  # tile > 64
+    assert lib.memt_gdn2_plan_count(i32([0, 130]), 2, 64, ctypes.byref(n)) == _lib.OK and n.value == 3
+    out = [(ctypes.c_int32 * 3)() for _ in range(4)]
+    offs = (ctypes.c_int32 * 2)()
+    ev = i32([0, 130])
+    # chunk count that does not match the boundaries, and read boundaries that do not span the tokens
+    assert lib.memt_gdn2_plan_build(ev, 2, ev, 2, ev, 2, None, 64, 2, out[0], out[1], offs, out[2], out[3],
+                                    None, None, None) == _lib.EINVAL
+    assert lib.memt_gdn2_plan_build(i32([0, 100]), 2, ev, 2, ev, 2, None, 64, 3, out[0], out[1], offs, out[2],
+                                    out[3], None, None, None) == _lib.EINVAL
+    assert lib.memt_gdn2_plan_build(ev, 2, ev, 2, ev, 2, None, 64, 3, out[0], out[1], offs, out[2], out[3],
+                                    None, None, None) == _lib.OK
+    assert list(out[0]) == [0, 64, 128] and list(out[1]) == [64, 64, 2] and list(offs) == [0, 3]
