@@ -209,3 +209,21 @@ def test_varlen_full_size_workload(dev):
         o1, h1 = memt_gdn2.chunk_gdn2(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b],
                                       initial_state=h0[n:n + 1], out_mode="causal")
         assert O.max_rel_err(host(ht[n]), host(h1[0])) <= TOL, n
+
+
+def test_empty_segments_and_empty_input(dev):
+    """A zero-length sequence keeps its initial state; a zero-token launch
+    returns an empty output and the initial states unchanged."""
+    T, H, D = 250, 2, 64
+    cu = [0, 100, 100, 250]
+    inp = O.synth_inputs(T, H, D, D, seed=71, h0_std=0.1, n_seq=3)
+    q, k, v, g, beta, h0 = _dev_inputs(inp, dev)
+    o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu, out_mode="causal")
+    o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], h0=inp["h0"],
+                                    cu_seqlens=cu)
+    assert np.array_equal(host(ht[1]), inp["h0"][1])
+    assert O.max_rel_err(host(ht), h_ref) <= TOL
+    assert O.parity_err(host(o), o_ref, out_bf16=True) <= TOL
+    z = lambda t: t[:, :0].contiguous()  # noqa: E731
+    o0, ht0 = memt_gdn2.chunk_gdn2(z(q), z(k), z(v), z(g), z(beta), initial_state=h0[:1], out_mode="causal")
+    assert o0.shape == (1, 0, H, D) and torch.equal(ht0, h0[:1])
