@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 4
+#define MEMT_GDN2_ABI_VERSION 5
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -141,6 +141,27 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
                            int out_mode, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * memt_gdn2_chunk_update on a pool of state slots, in place: no gather of the
+ * states before the call and no scatter of the final states after it.
+ * Replaces the executor's torch.cat gather and index_copy_ write-back around
+ * the memory block (runtime/executor.py:86-110).
+ *   pool     [n_slots, H, K, V] fp32
+ *   h0_slot  [n_seq] slot of each sequence's initial state (write_states)
+ *   ht_slot  [n_seq] slot that receives each sequence's final state
+ *   read_slot [n_block] slot each read block reads (out_mode = SNAPSHOT)
+ * A final state may go to the slot its initial state or its read comes from:
+ * the read completes before the update starts, and every initial state is
+ * read before any final state is written.  Distinct sequences must not share
+ * a ht_slot.  Slot indices are trusted (0 <= slot < n_slots).
+ */
+int memt_gdn2_chunk_update_slots(const void* q, const void* k, const void* v, const float* g,
+                                 const void* beta, int beta_dtype, const void* b, float* pool,
+                                 int n_slots, const int32_t* read_slot, const int32_t* h0_slot,
+                                 const int32_t* ht_slot, void* o, const memt_gdn2_plan* plan, int64_t T,
+                                 int H, int K, int V, float scale, int out_mode, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/*
  * WY stage only (replaces chunk_gdn2_fwd_intra, _vendor/fla/ops/gdn2/chunk_intra.py:693-787),
  * writing the reference layouts: w, kg [T,H,K] bf16, u [T,H,V] bf16, Akk [T,H,64] bf16
  * (the inverse (I+L)^-1), Aqk [T,H,64] bf16 (scale included; needs q), qg [T,H,K] bf16
@@ -173,6 +194,15 @@ int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* g
  */
 int memt_gdn2_read_fwd(const void* q, const float* snaps, void* o, const memt_gdn2_plan* plan,
                        int64_t T, int H, int K, int V, float scale, void* stream);
+
+/*
+ * memt_gdn2_read_fwd reading block b's state from pool slot read_slot[b]
+ * (pool [n_slots, H, K, V] fp32, read_slot [n_block] trusted in range): the
+ * query path without the executor's torch.cat gather (runtime/executor.py:86-91).
+ */
+int memt_gdn2_read_fwd_slots(const void* q, const float* pool, int n_slots, const int32_t* read_slot,
+                             void* o, const memt_gdn2_plan* plan, int64_t T, int H, int K, int V,
+                             float scale, void* stream);
 
 /*
  * MemTRMSNormGated (models/qwen/layer.py:15-31): for each row of x [rows, dim] bf16,

@@ -97,10 +97,15 @@ size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int 
   return group_layout(wy, n_chunk, n_seq, H, K, V, nullptr, nullptr);
 }
 
-int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta,
-                           int beta_dtype, const void* b, const float* h0, float* ht, const float* read_states,
-                           float* snaps, void* o, const memt_gdn2_plan* plan, int64_t T, int H, int K, int V,
-                           float scale, int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_dtype,
+                 const void* b, const float* h0, float* ht, const float* read_states, float* snaps, void* o,
+                 const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale, int out_mode,
+                 void* workspace, size_t workspace_bytes, void* stream, const int32_t* read_slot,
+                 const int32_t* h0_slot, const int32_t* ht_slot) {
   if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
   if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
   if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
@@ -125,8 +130,9 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
   const WyBuffers buf = wy_buffers(workspace, lay, causal);
 
   if (out_mode == MEMT_GDN2_OUT_SNAPSHOT) {
+    // before the scan: with slots, the read may name the slot the update overwrites
     hipError_t e = launch_read_fwd((const __bf16*)q, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
-                                   plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st);
+                                   plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st, read_slot);
     if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
   }
   WyArgs wa{};
@@ -154,6 +160,8 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
   sa.chunk_flags = plan->chunk_flags;
   sa.h0 = h0;
   sa.ht = ht;
+  sa.h0_slot = h0 ? h0_slot : nullptr;
+  sa.ht_slot = ht ? ht_slot : nullptr;
   sa.snaps = snaps;
   sa.o = causal ? (__bf16*)o : nullptr;
   sa.H = H;
@@ -163,6 +171,31 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
   sa.group_L = scan_group_chunks(plan->n_chunk, plan->n_seq, H, V);
   group_layout(lay.total, plan->n_chunk, plan->n_seq, H, K, V, &sa.grp, workspace);
   return status_of(launch_state(sa, K, V, causal, st));
+}
+
+}  // namespace
+
+extern "C" {
+
+int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                           int beta_dtype, const void* b, const float* h0, float* ht, const float* read_states,
+                           float* snaps, void* o, const memt_gdn2_plan* plan, int64_t T, int H, int K, int V,
+                           float scale, int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
+  return chunk_update(q, k, v, g, beta, beta_dtype, b, h0, ht, read_states, snaps, o, plan, T, H, K, V, scale,
+                      out_mode, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int memt_gdn2_chunk_update_slots(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                 int beta_dtype, const void* b, float* pool, int n_slots, const int32_t* read_slot,
+                                 const int32_t* h0_slot, const int32_t* ht_slot, void* o,
+                                 const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale,
+                                 int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
+  if (pool == nullptr || n_slots <= 0 || h0_slot == nullptr || ht_slot == nullptr) return MEMT_GDN2_EINVAL;
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && read_slot == nullptr) return MEMT_GDN2_EINVAL;
+  if (!aligned16(pool)) return MEMT_GDN2_EINVAL;
+  return chunk_update(q, k, v, g, beta, beta_dtype, b, pool, pool, pool, nullptr, o, plan, T, H, K, V, scale,
+                      out_mode, workspace, workspace_bytes, stream,
+                      out_mode == MEMT_GDN2_OUT_SNAPSHOT ? read_slot : nullptr, h0_slot, ht_slot);
 }
 
 int memt_gdn2_wy_fwd(const void* q, const void* k, const void* v, const float* gk, const void* b, const void* beta,
@@ -246,6 +279,18 @@ int memt_gdn2_read_fwd(const void* q, const float* snaps, void* o, const memt_gd
   if (!aligned16(q) || !aligned16(snaps)) return MEMT_GDN2_EINVAL;
   return status_of(launch_read_fwd((const __bf16*)q, snaps, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
                                    plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, (hipStream_t)stream));
+}
+
+int memt_gdn2_read_fwd_slots(const void* q, const float* pool, int n_slots, const int32_t* read_slot, void* o,
+                             const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale, void* stream) {
+  if (pool == nullptr || n_slots <= 0 || read_slot == nullptr) return MEMT_GDN2_EINVAL;
+  if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (plan->n_chunk > 0 && (q == nullptr || o == nullptr || plan->chunk_block_ids == nullptr)) return MEMT_GDN2_EINVAL;
+  if (!aligned16(q) || !aligned16(pool)) return MEMT_GDN2_EINVAL;
+  return status_of(launch_read_fwd((const __bf16*)q, pool, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
+                                   plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, (hipStream_t)stream,
+                                   read_slot));
 }
 
 int memt_gdn2_rms_norm_gated(const void* x, const void* gate, const void* weight, void* out, int64_t rows, int dim,

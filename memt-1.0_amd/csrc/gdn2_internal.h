@@ -171,8 +171,10 @@ struct StateArgs {
   const int32_t* seq_chunk_offsets;
   const int32_t* chunk_block_ids;
   const int32_t* chunk_flags;
-  const float* h0;     // [N,H,K,V] or null
-  float* ht;           // [N,H,K,V] or null
+  const float* h0;     // [N,H,K,V] or null; with h0_slot, [slots,H,K,V] indexed by h0_slot[seq]
+  float* ht;           // [N,H,K,V] or null; with ht_slot, [slots,H,K,V] indexed by ht_slot[seq]
+  const int32_t* h0_slot;  // [N] or null
+  const int32_t* ht_slot;  // [N] or null
   float* snaps;        // [n_block,H,K,V] or null
   __bf16* o;           // [T,H,V] (causal) or null
   int H;
@@ -212,7 +214,7 @@ hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bo
 hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream_t stream);
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
-                           int K, int V, float scale, hipStream_t stream);
+                           int K, int V, float scale, hipStream_t stream, const int32_t* block_slot = nullptr);
 hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
                           const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
                           float eps, float softcap, int gate_kind, hipStream_t stream);

@@ -14,13 +14,14 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
                                                        const float* __restrict__ snaps,
                                                        __bf16* __restrict__ o, const int32_t* chunk_tok0,
                                                        const int32_t* chunk_len, const int32_t* block_ids,
-                                                       int H, float scale) {
+                                                       int H, float scale, const int32_t* block_slot) {
   constexpr int SKP = K + 8;
   __shared__ __attribute__((aligned(16))) __bf16 S_lds[V * SKP];  // column-major bf16(S)
   const int chunk = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
-  const float* Sp = snaps + ((size_t)block_ids[chunk] * H + h) * K * V;
+  const int blk = block_ids[chunk];
+  const float* Sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V;
   for (int idx = tid; idx < K * V / 4; idx += 256) {
     const int row = idx / (V / 4), c4 = (idx % (V / 4)) * 4;
     const f32x4 s4 = *(const f32x4*)(Sp + (size_t)row * V + c4);
@@ -294,18 +295,18 @@ __global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const _
 
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
-                           int K, int V, float scale, hipStream_t stream) {
+                           int K, int V, float scale, hipStream_t stream, const int32_t* block_slot) {
   if (n_chunk == 0) return hipSuccess;
   dim3 grid(n_chunk, H), block(256);
   if (K == 64 && V == 64)
     hipLaunchKernelGGL((read_fwd_kernel<64, 64>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale);
+                       chunk_block_ids, H, scale, block_slot);
   else if (K == 128 && V == 128)
     hipLaunchKernelGGL((read_fwd_kernel<128, 128>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale);
+                       chunk_block_ids, H, scale, block_slot);
   else if (K == 256 && V == 256)
     hipLaunchKernelGGL((read_fwd_kernel<256, 256>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale);
+                       chunk_block_ids, H, scale, block_slot);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -161,7 +161,10 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 
   // S tile (rt, ct): rows 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr
   f32x4 S[RT][CT];
-  if (MODE == 0 && !first) {
+  // Every group of a multi-group sequence starts from the combine's S0 (the
+  // first one from the combine's copy of h0), so when ht and h0 name the same
+  // slot the last group's ht write cannot overtake the first group's h0 read.
+  if (MODE == 0 && !(first && last)) {
     // the group's start state from the combine, in C-frag order
     const float* s0 = a.grp.S0 + ((size_t)unitg * H + h) * K * V;
 #pragma unroll
@@ -170,7 +173,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       for (int ct = 0; ct < CT; ++ct)
         S[rt][ct] = *(const f32x4*)(s0 + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
   } else {
-    const float* h0p = (MODE == 0 && a.h0 != nullptr) ? a.h0 + ((size_t)seq * H + h) * K * V : nullptr;
+    const int slot = a.h0_slot ? a.h0_slot[seq] : seq;
+    const float* h0p = (MODE == 0 && a.h0 != nullptr) ? a.h0 + ((size_t)slot * H + h) * K * V : nullptr;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -416,7 +420,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       for (int ct = 0; ct < CT; ++ct)
         *(f32x4*)(qo + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4) = S[rt][ct];
   } else if (last && a.ht != nullptr) {
-    float* out = a.ht + ((size_t)seq * H + h) * K * V;
+    float* out = a.ht + ((size_t)(a.ht_slot ? a.ht_slot[seq] : seq) * H + h) * K * V;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -493,7 +497,7 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   const int v0 = vs * BV, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
 
   f32x4 S[RT][CT];
-  const float* h0p = a.h0 ? a.h0 + ((size_t)n * H + h) * K * V : nullptr;
+  const float* h0p = a.h0 ? a.h0 + ((size_t)(a.h0_slot ? a.h0_slot[n] : n) * H + h) * K * V : nullptr;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -505,6 +509,15 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
       }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): settle h0 before the prefetching loop
   asm volatile("" ::: "memory");
+  {
+    // the first group's start state: the scan reads it here, never from h0
+    float* S0 = a.grp.S0 + ((size_t)g0 * H + h) * K * V;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        *(f32x4*)(S0 + ((size_t)((w * RT + rt) * (V / 16) + (v0 >> 4) + ct) * 64 + lane) * 4) = S[rt][ct];
+  }
 
   // First load, in the order the loop consumes and reloads the fragments: the
   // empty asm statements keep the compiler from reordering the loads, so the

@@ -28,7 +28,9 @@ from .ops import (
     snapshot_read,
     token_memory_packed,
     memory_prologue,
+    read_slots,
     token_memory_packed_flash,
+    token_memory_packed_slots,
     workspace_bytes,
     write_gates,
 )
@@ -62,4 +64,6 @@ __all__ = [
     "workspace_bytes",
     "write_gates",
     "memory_prologue",
+    "read_slots",
+    "token_memory_packed_slots",
 ]

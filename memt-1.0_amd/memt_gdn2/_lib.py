@@ -33,7 +33,7 @@ OUT_CAUSAL = 2
 CHUNK_BLOCK_START = 1
 CHUNK_COMMIT = 2
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class Plan(ctypes.Structure):
@@ -70,12 +70,17 @@ _SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
     ),
+    "memt_gdn2_chunk_update_slots": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
     "memt_gdn2_wy_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _PLAN, _I64, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
     "memt_gdn2_fwd_h": (_I, [_P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "memt_gdn2_read_fwd": (_I, [_P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _P]),
+    "memt_gdn2_read_fwd_slots": (_I, [_P, _P, _I, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _P]),
     "memt_gdn2_rms_norm_gated": (_I, [_P, _P, _P, _P, _I64, _I, _F, _F, _I, _P]),
     "memt_gdn2_readout_fused": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _I, _P]),
     "memt_gdn2_plan_count": (_I, [_P, _I, _I, _P]),

@@ -21,7 +21,8 @@ from torch.nn import functional as F
 
 from .layout import WY_TILE_TOKENS, build_chunk_plan, validate_packed_inputs
 from .norm import MemTRMSNormGated
-from .ops import l2norm, memory_prologue, memt_gdn2_read_fwd, token_memory_packed
+from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, token_memory_packed,
+                  token_memory_packed_slots)
 
 
 class QwenMemoryBlock(nn.Module):
@@ -88,6 +89,40 @@ class QwenMemoryBlock(nn.Module):
             scale=self.read_scale, chunk_tokens=self.chunk_tokens)
         output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
         return output.view(T, self.value_dim), next_state
+
+    @torch.no_grad()
+    def packed_slots(self, hidden_states, pool, read_slot, write_slot, *, lengths, commit):
+        """``packed`` on a state pool in place: sample ``n`` reads
+        ``pool[read_slot[n]]`` and, when committing, scans from
+        ``pool[write_slot[n]]`` and leaves its final state there.  ``pool`` is
+        ``[slots, H, D, D]`` or ``[slots, 1, H, D, D]`` fp32.  Returns the
+        residual ``[T, H*D]`` bf16."""
+        T, H, D = len(hidden_states), self.num_heads, self.head_dim
+        if hidden_states.ndim != 2 or hidden_states.shape[1] != self.hidden_size or \
+                hidden_states.dtype != torch.bfloat16 or not hidden_states.is_cuda:
+            raise ValueError("Memory expects CUDA BF16 hidden states [tokens, hidden_size]")
+        if not lengths or any(n <= 0 for n in lengths) or sum(lengths) != T:
+            raise ValueError("Packed sample lengths must cover the hidden token rows")
+        if pool.device != hidden_states.device or pool.dtype != torch.float32 or pool.shape[-3:] != (H, D, D):
+            raise ValueError(f"Memory expects an FP32 state pool [slots, ..., {H}, {D}, {D}] on the hidden device")
+        hidden_batch = hidden_states.unsqueeze(0)
+        weight = self.in_proj.weight
+        q, k, v = F.linear(hidden_batch, weight[: self.qkv_width]).split(self.qkv_rows, dim=-1)
+        output_gate = self.g_down(F.linear(hidden_batch, weight[-D:]))
+        if not commit:
+            q_hat = l2norm(q.reshape(1, T, H, D))
+            read = read_slots(q_hat, pool, read_slot, lengths, self.read_scale)
+            output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
+            return output.view(T, self.value_dim)
+        erase, write, decay_latent = torch.split(
+            F.linear(hidden_batch, weight[self._write_gate_slice]), self.write_gate_rows, dim=-1)
+        decay = self.f_down(decay_latent)
+        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H)
+        read = token_memory_packed_slots(q_hat, k_til, v.reshape(1, T, H, D), g, beta, pool, read_slot, write_slot,
+                                         erase=None, lengths=lengths, scale=self.read_scale,
+                                         chunk_tokens=self.chunk_tokens)
+        output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
+        return output.view(T, self.value_dim)
 
     def forward(self, hidden_states, initial_state, *, commit):
         """Single-request entry (models/qwen/layer.py:154-161)."""

@@ -32,6 +32,8 @@ __all__ = [
     "workspace_bytes",
     "write_gates",
     "memory_prologue",
+    "token_memory_packed_slots",
+    "read_slots",
 ]
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
@@ -501,3 +503,100 @@ def memory_prologue(q, k, decay, decay_bias, decay_scale_log, erase, write, num_
         "memory_prologue",
     )
     return q_hat, k_til, beta, g
+
+
+# ---------------------------------------------------------------------------
+# Slot-indexed state I/O (the executor's gather and write-back folded in)
+# ---------------------------------------------------------------------------
+
+
+def _pool_view(pool: torch.Tensor, H: int, K: int, V: int) -> torch.Tensor:
+    """A state pool ``[slots, H, K, V]`` (or the runtime's ``[slots, 1, H, K, V]``)
+    as the contiguous fp32 ``[slots, H, K, V]`` the kernels index in place."""
+    if pool.dtype != torch.float32 or not pool.is_contiguous() or pool.shape[-3:] != (H, K, V):
+        raise ValueError(f"state pool must be contiguous fp32 [slots, ..., {H}, {K}, {V}]")
+    return pool.view(-1, H, K, V)
+
+
+def _slot_index(slots, n: int, n_slots: int, device, name: str, distinct: bool = False) -> torch.Tensor:
+    """Slot indices as device int32.  Host indices are range-checked here;
+    device tensors are trusted (checking them would copy them back)."""
+    if isinstance(slots, torch.Tensor) and slots.is_cuda:
+        if slots.dtype != torch.int32 or slots.shape != (n,):
+            raise ValueError(f"{name} must be int32 [{n}]")
+        return slots.contiguous()
+    host = torch.as_tensor(slots, dtype=torch.int64).reshape(-1)
+    if host.numel() != n or (n and (int(host.min()) < 0 or int(host.max()) >= n_slots)):
+        raise ValueError(f"{name} must hold {n} indices into the {n_slots} state slots")
+    if distinct and len(set(host.tolist())) != n:
+        raise ValueError(f"{name} must not repeat a slot")
+    return host.to(device=device, dtype=torch.int32)
+
+
+def token_memory_packed_slots(q, k, v, log_decay, write, pool, read_slots, write_slots, *, erase, lengths, scale,
+                              chunk_tokens):
+    """``token_memory_packed`` on a state pool, in place: sample ``n`` scans
+    from ``pool[write_slots[n]]``, its final state replaces that slot, and its
+    tokens read ``pool[read_slots[n]]`` as it was before the call.  This is the
+    executor's commit pass (runtime/executor.py:83-110) without the
+    ``torch.cat`` gather and the ``index_copy_`` write-back.  Returns ``read``."""
+    if not lengths or any(int(n) <= 0 for n in lengths):
+        raise ValueError("Packed sample lengths must be positive")
+    lib = _lib.load()
+    _, T, H, K = k.shape
+    V = v.shape[-1]
+    _lib.require_gpu(q, k, v, log_decay, write, erase, pool)
+    pv = _pool_view(pool, H, K, V)
+    plan = packed_plan(lengths, k.device, chunk_tokens=chunk_tokens)
+    N = plan.num_sample
+    rs = _slot_index(read_slots, N, pv.shape[0], k.device, "read_slots")
+    ws_ = _slot_index(write_slots, N, pv.shape[0], k.device, "write_slots", distinct=True)
+    for name, t, D in (("q", q, K), ("k", k, K), ("v", v, V), ("log_decay", log_decay, K), ("write", write, V)):
+        _check_tokens(name, t, T, H, D)
+    if erase is not None:
+        _check_tokens("erase", erase, T, H, K)
+    for name, t, dt in (("q", q, torch.bfloat16), ("k", k, torch.bfloat16), ("v", v, torch.bfloat16),
+                        ("log_decay", log_decay, torch.float32), ("erase", erase, torch.bfloat16)):
+        if t is not None and t.dtype != dt:
+            raise ValueError(f"{name} must be {dt}, got {t.dtype}")
+    if write.dtype not in _DT:
+        raise ValueError("write gate must be bf16 or fp32")
+    q, k, v, log_decay, write, erase = _contig(q, k, v, log_decay, write, erase)
+    o = torch.empty(1, T, H, V, dtype=torch.bfloat16, device=k.device)
+    ws = _workspace(k.device, workspace_bytes(plan.num_chunk, H, K, V, "snapshot", N))
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_chunk_update_slots(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), log_decay.data_ptr(), write.data_ptr(), _DT[write.dtype],
+            _lib.ptr(erase), pv.data_ptr(), pv.shape[0], rs.data_ptr(), ws_.data_ptr(), ws_.data_ptr(), o.data_ptr(),
+            ctypes.byref(p), T, H, K, V, float(scale), _OUT["snapshot"], ws.data_ptr(), ws.numel(),
+            _lib.stream_of(k.device)),
+        "chunk_update_slots",
+    )
+    return o
+
+
+def read_slots(q, pool, read_slots_, lengths, scale):
+    """Every token of sample ``n`` reads ``bf16(scale * q . bf16(pool[read_slots[n]]))``
+    (models/qwen/ops/read.py:10-39 on the pool in place)."""
+    lib = _lib.load()
+    _lib.require_gpu(q, pool)
+    _, T, H, K = q.shape
+    pv = _pool_view(pool, H, K, pool.shape[-1])
+    V = pv.shape[-1]
+    samples = [0]
+    for n in lengths:
+        samples.append(samples[-1] + int(n))
+    if samples[-1] != T:
+        raise ValueError("lengths must cover the query tokens")
+    plan = build_chunk_plan(samples, samples, device=q.device)
+    rs = _slot_index(read_slots_, plan.num_block, pv.shape[0], q.device, "read_slots")
+    (q,) = _contig(q)
+    out = torch.empty(1, T, H, V, device=q.device, dtype=torch.bfloat16)
+    p = plan.abi()
+    _lib.check(
+        lib.memt_gdn2_read_fwd_slots(q.data_ptr(), pv.data_ptr(), pv.shape[0], rs.data_ptr(), out.data_ptr(),
+                                     ctypes.byref(p), T, H, K, V, float(scale), _lib.stream_of(q.device)),
+        "read_fwd_slots",
+    )
+    return out

@@ -18,7 +18,11 @@ of the same step.  Slot state lives in ``pool.storage[layer]``, a tensor
 
 The gather is ``index_select`` on a device index tensor and the scatter
 ``index_copy_``, one kernel each, where the reference concatenates per-slot
-views (executor.py:86-91).  The values moved are the same.
+views (executor.py:86-91).  The values moved are the same.  With
+``slot_io=True`` and a block that has ``packed_slots``, neither happens: the
+kernels read the slots in place and write each commit's final state into its
+slot (the read and every initial state are consumed before any final state
+is stored).
 """
 
 from __future__ import annotations
@@ -63,8 +67,9 @@ class MemoryRuntime:
     the transaction's candidate slot for a commit); ``memory_read`` maps a
     session to whether its queries read memory."""
 
-    def __init__(self, pool):
+    def __init__(self, pool, *, slot_io: bool = False):
         self.pool = pool
+        self.slot_io = slot_io
         self.plan: StepPlan | None = None
         self._layers: set[int] = set()
         self.slot_of: Mapping[str, int] = {}
@@ -116,15 +121,21 @@ class MemoryRuntime:
                 continue
             rows = torch.cat([torch.arange(s.start, s.stop) for s in samples]).to(dev)
             lengths = [s.stop - s.start for s in samples]
-            slots = torch.tensor([self.slot_of[s.request.rid] for s in samples], dtype=torch.int64).to(dev)
-            # a copy: the scan's initial state, so `final` may replace the slot afterwards
-            states = storage.index_select(0, slots).view(len(samples), *storage.shape[2:])
-            residual, final = compute.packed(hidden.index_select(0, rows), states, lengths=lengths, commit=commit,
-                                             write_states=states)
+            slot_list = [self.slot_of[s.request.rid] for s in samples]
+            if self.slot_io and hasattr(compute, "packed_slots"):
+                residual = compute.packed_slots(hidden.index_select(0, rows), storage, slot_list, slot_list,
+                                                lengths=lengths, commit=commit)
+                final = None
+            else:
+                slots = torch.tensor(slot_list, dtype=torch.int64).to(dev)
+                # a copy: the scan's initial state, so `final` may replace the slot afterwards
+                states = storage.index_select(0, slots).view(len(samples), *storage.shape[2:])
+                residual, final = compute.packed(hidden.index_select(0, rows), states, lengths=lengths,
+                                                 commit=commit, write_states=states)
             if residual.shape != (len(rows), output.shape[1]) or residual.dtype != output.dtype:
                 raise RuntimeError("Packed memory output invariant violated")
             output.index_copy_(0, rows, residual)
-            if commit:
+            if commit and final is not None:
                 storage.index_copy_(0, slots, final.unsqueeze(1))
 
     def finish(self, success: bool) -> None:
