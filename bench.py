@@ -169,6 +169,60 @@ def bench_readout(dev, steps, warmup, B=64, H=16, D=128, gate_kind="softcap_silu
 COPY_BYTES = 1 << 30  # calibration copy: reads and writes exactly this many bytes
 
 
+def _event_ms(fn, reps, warmup=2):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_prologue(dev, reps=20, T=8192, H=16, D=128):
+    """The gate and q/k prologue of the memory block on raw projections, alone
+    (HBM: 20 D bytes per token and head) and as part of the commit path,
+    separate kernel vs folded into the update's WY kernel."""
+    import memt_gdn2
+
+    W = H * D
+    g = torch.Generator(device=dev).manual_seed(20261206)
+    qkv = torch.randn(T, 3 * W, generator=g, device=dev).to(torch.bfloat16)
+    gates = torch.randn(T, 2 * W + D, generator=g, device=dev).to(torch.bfloat16)
+    decay = torch.randn(T, W, generator=g, device=dev).to(torch.bfloat16)
+    bias = (torch.randn(W, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    rate = (torch.randn(H, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    q, k, v = qkv[:, :W], qkv[:, W:2 * W], qkv[:, 2 * W:]
+    erase, write = gates[:, :W], gates[:, W:2 * W]
+    st = torch.randn(1, H, D, D, generator=g, device=dev) * 0.02
+    pro_ms = _event_ms(lambda: memt_gdn2.memory_prologue(q, k, decay, bias, rate, erase, write, H), reps)
+    pro_bytes = T * H * 20 * D
+
+    def separate():
+        qh, kt, beta, gg = memt_gdn2.memory_prologue(q, k, decay, bias, rate, erase, write, H)
+        return memt_gdn2.token_memory_packed(qh, kt, v.reshape(1, T, H, D), gg, beta, st, st, erase=None,
+                                             lengths=[T], scale=D ** -0.5, chunk_tokens=2048)
+
+    def fused():
+        return memt_gdn2.token_memory_packed_fused(q, k, v, decay, bias, rate, erase, write, st, st, lengths=[T],
+                                                   scale=D ** -0.5, chunk_tokens=2048, num_heads=H)
+
+    sep_ms = _event_ms(separate, reps)
+    fus_ms = _event_ms(fused, reps)
+    return {
+        "workload": f"memory block commit from raw projections, T={T} H={H} d={D}, one sample, 2048-token events",
+        "prologue_us": pro_ms * 1e3,
+        "prologue_gbs": pro_bytes / (pro_ms * 1e-3) / 1e9,
+        "prologue_hbm_frac": pro_bytes / (pro_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "prologue_algorithmic_bytes": pro_bytes,
+        "commit_separate_prologue_ms": sep_ms,
+        "commit_fused_prologue_ms": fus_ms,
+    }
+
+
 def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32):
     """The wide-state Flash-like shape: chunked update (causal) and a batch-B readout."""
     steps = min(steps, 20)
@@ -298,6 +352,7 @@ def main():
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)
     snap = bench_update(dev, max(10, args.steps // 2), 2, T, H, D, out_mode="snapshot") if args.mode == "causal" else None
     ro = bench_readout(dev, args.steps, args.warmup)
+    pro = bench_prologue(dev)
 
     causal = args.mode == "causal"
     up_traffic, ro_traffic = profiled_traffic()
@@ -353,6 +408,7 @@ def main():
             "state_sets_rotated": ro["nsets"],
         },
     }
+    result["memory_block_commit"] = pro
     if snap is not None:
         result["snapshot_mode"] = {
             "workload": "token_memory_packed semantics (tokens read the incoming state), same shapes",

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 5
+#define MEMT_GDN2_ABI_VERSION 6
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -86,6 +86,31 @@ int memt_gdn2_plan_build(const int32_t* read, int n_read, const int32_t* sample,
                          int32_t* chunk_len, int32_t* sample_chunk_offsets,
                          int32_t* chunk_block_ids, int32_t* chunk_flags, int32_t* chunk_indices,
                          int32_t* chunk_is_block_start, int32_t* chunk_commits);
+
+/*
+ * Raw projection rows of the memory block (the outputs of its in_proj / f_down
+ * GEMMs, read in place): q, k, decay and erase rows hold H*K bf16 channels,
+ * v and write rows H*V; each tensor's rows are `*_stride` elements apart
+ * (a multiple of 4, at least the row width; pointers 8-byte aligned).
+ */
+typedef struct memt_gdn2_projections {
+  const void* q;
+  int64_t q_stride;
+  const void* k;
+  int64_t k_stride;
+  const void* v;
+  int64_t v_stride;
+  const void* decay; /* f_down(decay latent), pre-softplus */
+  int64_t decay_stride;
+  const void* erase; /* erase logits */
+  int64_t erase_stride;
+  const void* write; /* write logits */
+  int64_t write_stride;
+  const void* decay_bias;      /* [H*K] bf16 */
+  const void* decay_scale_log; /* [H] bf16 */
+  float eps;                   /* l2norm epsilon (1e-6) */
+  int32_t reserved;
+} memt_gdn2_projections;
 
 int memt_gdn2_abi_version(void);
 const char* memt_gdn2_strerror(int status);
@@ -160,6 +185,23 @@ int memt_gdn2_chunk_update_slots(const void* q, const void* k, const void* v, co
                                  const int32_t* ht_slot, void* o, const memt_gdn2_plan* plan, int64_t T,
                                  int H, int K, int V, float scale, int out_mode, void* workspace,
                                  size_t workspace_bytes, void* stream);
+
+/*
+ * The commit path of QwenMemoryBlock.packed from its raw projections in one
+ * update: the gate and q/k prologue (models/qwen/layer.py:71-97) runs inside
+ * the WY kernel (g = -exp(s_h) softplus(decay + bias), beta = bf16(sigmoid(write)),
+ * q_hat = l2norm(q), k_til = bf16(sqrt_b * l2norm(k)), unit erase gate), so no
+ * prologue tensor goes through HBM.  q_hat [T,H,K] bf16 receives l2norm(q)
+ * (required for out_mode SNAPSHOT, which reads it).  States as in
+ * memt_gdn2_chunk_update, or, when h0_slot / ht_slot (and read_slot) are not
+ * NULL, a pool of n_slots states addressed as in memt_gdn2_chunk_update_slots
+ * (h0, ht and read_states then name the same pool).
+ */
+int memt_gdn2_chunk_update_fused(const memt_gdn2_projections* x, void* q_hat, const float* h0, float* ht,
+                                 const float* read_states, int n_slots, const int32_t* read_slot,
+                                 const int32_t* h0_slot, const int32_t* ht_slot, void* o,
+                                 const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale,
+                                 int out_mode, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * WY stage only (replaces chunk_gdn2_fwd_intra, _vendor/fla/ops/gdn2/chunk_intra.py:693-787),

@@ -101,12 +101,37 @@ size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int 
 
 namespace {
 
+bool raw_row_ok(const void* p, int64_t stride, int64_t width) {
+  return p != nullptr && ((uintptr_t)p & 7u) == 0 && stride >= width && stride % 4 == 0;
+}
+
 int chunk_update(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_dtype,
                  const void* b, const float* h0, float* ht, const float* read_states, float* snaps, void* o,
                  const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale, int out_mode,
                  void* workspace, size_t workspace_bytes, void* stream, const int32_t* read_slot,
-                 const int32_t* h0_slot, const int32_t* ht_slot) {
+                 const int32_t* h0_slot, const int32_t* ht_slot, const memt_gdn2_projections* x = nullptr,
+                 void* q_hat = nullptr) {
   if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
+  if (x != nullptr) {
+    // raw projections: the prologue runs inside the WY kernel
+    if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
+    const int64_t wk = (int64_t)H * K, wv = (int64_t)H * V;
+    if (plan->n_chunk > 0) {
+      if (!raw_row_ok(x->q, x->q_stride, wk) || !raw_row_ok(x->k, x->k_stride, wk) ||
+          !raw_row_ok(x->v, x->v_stride, wv) || !raw_row_ok(x->decay, x->decay_stride, wk) ||
+          !raw_row_ok(x->erase, x->erase_stride, wk) || !raw_row_ok(x->write, x->write_stride, wv) ||
+          x->decay_bias == nullptr || ((uintptr_t)x->decay_bias & 7u) || x->decay_scale_log == nullptr)
+        return MEMT_GDN2_EINVAL;
+      if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && q_hat == nullptr) return MEMT_GDN2_EINVAL;
+    }
+    q = x->q;
+    k = x->k;
+    v = x->v;
+    g = (const float*)x->decay;  // placeholders for the checks below; the kernel reads the raw rows
+    beta = x->write;
+    beta_dtype = MEMT_GDN2_BF16;
+    b = nullptr;
+  }
   if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
   if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
   if (out_mode != MEMT_GDN2_OUT_NONE && out_mode != MEMT_GDN2_OUT_SNAPSHOT && out_mode != MEMT_GDN2_OUT_CAUSAL)
@@ -114,7 +139,8 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   if (plan->n_chunk > 0) {
     if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || plan->seq_chunk_offsets == nullptr)
       return MEMT_GDN2_EINVAL;
-    if (!aligned16(k) || !aligned16(v) || (b && !aligned16(b)) || (q && !aligned16(q))) return MEMT_GDN2_EINVAL;
+    if (x == nullptr && (!aligned16(k) || !aligned16(v) || (b && !aligned16(b)) || (q && !aligned16(q))))
+      return MEMT_GDN2_EINVAL;
     if (out_mode != MEMT_GDN2_OUT_NONE && (q == nullptr || o == nullptr)) return MEMT_GDN2_EINVAL;
     if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && (read_states == nullptr || plan->chunk_block_ids == nullptr))
       return MEMT_GDN2_EINVAL;
@@ -129,7 +155,7 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   hipStream_t st = (hipStream_t)stream;
   const WyBuffers buf = wy_buffers(workspace, lay, causal);
 
-  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT) {
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x == nullptr) {
     // before the scan: with slots, the read may name the slot the update overwrites
     hipError_t e = launch_read_fwd((const __bf16*)q, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
                                    plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st, read_slot);
@@ -148,8 +174,30 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   wa.scale = scale;
   wa.out = buf;
   wa.A_ref = nullptr;
+  if (x != nullptr) {
+    wa.q = (const __bf16*)x->q;
+    wa.f_raw = (const __bf16*)x->decay;
+    wa.e_raw = (const __bf16*)x->erase;
+    wa.w_raw = (const __bf16*)x->write;
+    wa.decay_bias = (const __bf16*)x->decay_bias;
+    wa.decay_scale_log = (const __bf16*)x->decay_scale_log;
+    wa.q_hat = (__bf16*)q_hat;
+    wa.q_stride = x->q_stride;
+    wa.k_stride = x->k_stride;
+    wa.v_stride = x->v_stride;
+    wa.f_stride = x->decay_stride;
+    wa.e_stride = x->erase_stride;
+    wa.w_stride = x->write_stride;
+    wa.eps = x->eps;
+  }
   hipError_t e = launch_wy(wa, plan->n_chunk, K, V, causal, false, beta_dtype == MEMT_GDN2_BF16, st);
   if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x != nullptr) {
+    // q_hat comes from the WY kernel; the read still precedes the scan
+    e = launch_read_fwd((const __bf16*)q_hat, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
+                        plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st, read_slot);
+    if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
+  }
 
   StateArgs sa{};
   sa.in = buf;
@@ -183,6 +231,23 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
                            float scale, int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
   return chunk_update(q, k, v, g, beta, beta_dtype, b, h0, ht, read_states, snaps, o, plan, T, H, K, V, scale,
                       out_mode, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int memt_gdn2_chunk_update_fused(const memt_gdn2_projections* x, void* q_hat, const float* h0, float* ht,
+                                 const float* read_states, int n_slots, const int32_t* read_slot,
+                                 const int32_t* h0_slot, const int32_t* ht_slot, void* o,
+                                 const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale,
+                                 int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr) return MEMT_GDN2_EINVAL;
+  const bool slots = h0_slot != nullptr || ht_slot != nullptr || read_slot != nullptr;
+  if (slots) {
+    if (n_slots <= 0 || h0_slot == nullptr || ht_slot == nullptr || h0 == nullptr || h0 != ht) return MEMT_GDN2_EINVAL;
+    if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && (read_slot == nullptr || read_states != h0)) return MEMT_GDN2_EINVAL;
+  }
+  return chunk_update(nullptr, nullptr, nullptr, nullptr, nullptr, MEMT_GDN2_BF16, nullptr, h0, ht, read_states,
+                      nullptr, o, plan, T, H, K, V, scale, out_mode, workspace, workspace_bytes, stream,
+                      slots && out_mode == MEMT_GDN2_OUT_SNAPSHOT ? read_slot : nullptr, slots ? h0_slot : nullptr,
+                      slots ? ht_slot : nullptr, x, q_hat);
 }
 
 int memt_gdn2_chunk_update_slots(const void* q, const void* k, const void* v, const float* g, const void* beta,

@@ -36,6 +36,32 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
 // Native v_exp_f32 (base 2).  Inputs below -126 give denormal/zero results.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Gate transcendentals on the hardware exp2 / log2 / rcp, a few fp32 ulp from
+// the correctly rounded values (the gates' bf16 outputs round that away).
+// exp(x) = 2^(x log2 e): the product is carried as hi + lo (log2 e split in
+// two fp32 parts, fma for the rounding of x * hi), and 2^lo ~ 1 + lo ln 2.
+__device__ __forceinline__ float gate_exp(float x) {
+  constexpr float kL2eHi = 1.44269502f, kL2eLo = 1.92596299e-8f, kLn2 = 0.693147182f;
+  const float p = x * kL2eHi;
+  const float lo = fmaf(x, kL2eHi, -p) + x * kL2eLo;
+  return __builtin_amdgcn_exp2f(p) * fmaf(lo, kLn2, 1.f);
+}
+// log1p(y) for y >= 0: log(u) * y / (u - 1) with u = 1 + y, which cancels the
+// rounding of u (D. Goldberg, "What every computer scientist should know about
+// floating-point arithmetic", 1991, Theorem 4).
+__device__ __forceinline__ float gate_log1p(float y) {
+  const float u = 1.f + y;
+  if (u == 1.f) return y;
+  return __builtin_amdgcn_logf(u) * 0.693147182f * (y * __builtin_amdgcn_rcpf(u - 1.f));
+}
+// torch.nn.functional.softplus (beta 1, threshold 20), as max(x, 0) + log1p(e^-|x|)
+__device__ __forceinline__ float softplus20(float x) {
+  return x > 20.f ? x : fmaxf(x, 0.f) + gate_log1p(gate_exp(-fabsf(x)));
+}
+// torch.nn.functional.logsigmoid: min(x, 0) - log1p(e^-|x|)
+__device__ __forceinline__ float logsigmoid(float x) { return fminf(x, 0.f) - gate_log1p(gate_exp(-fabsf(x))); }
+__device__ __forceinline__ float gate_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + gate_exp(-x)); }
+
 __device__ __forceinline__ float bf16_to_f32(__bf16 x) { return (float)x; }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 

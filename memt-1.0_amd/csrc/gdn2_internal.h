@@ -106,6 +106,16 @@ struct WyArgs {
   float scale;
   WyBuffers out;
   __bf16* A_ref;       // optional [T,H,64] bf16 inverse (reference layout)
+  // raw projections (f_raw != null): q, k, v are then projection rows with the
+  // strides below, g and beta come from f_raw / w_raw, b must be null
+  const __bf16* f_raw;           // decay projection [T, f_stride]
+  const __bf16* e_raw;           // erase logits [T, e_stride]
+  const __bf16* w_raw;           // write logits [T, w_stride]
+  const __bf16* decay_bias;      // [H*K]
+  const __bf16* decay_scale_log; // [H]
+  __bf16* q_hat;                 // [T,H,K] normalised q out, or null
+  int64_t q_stride, k_stride, v_stride, f_stride, e_stride, w_stride;
+  float eps;
 };
 
 // Two-level scan.  A sequence's chunks are split into groups of L chunks.

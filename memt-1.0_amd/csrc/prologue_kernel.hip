@@ -8,10 +8,10 @@
 //   q_hat  = bf16(q / sqrt(sum q^2 + 1e-6))               bf16   (l2norm_fwd, :92-94)
 //   k_til  = bf16(f32(sqrt_b) * f32(bf16(k / sqrt(sum k^2 + 1e-6))))   (:95-96)
 // Here one kernel reads each input row once and writes each output once.
-// The fp32 arithmetic follows the reference's op order (each torch op is one
-// fp32 rounding), so the bf16 outputs agree with it except where a
-// transcendental's last-bit difference moves a value across a bf16 rounding
-// boundary (one bf16 ulp).
+// The fp32 arithmetic follows the reference's op order, with the
+// transcendentals on the hardware exp2 / log2 / rcp (a few fp32 ulp), so the
+// bf16 outputs agree with the reference's except where that difference moves
+// a value across a bf16 rounding boundary (one bf16 ulp).
 //
 // Layout: a lane owns 8 consecutive channels of one (token, head) row, so
 // each load and store is 16 bytes and a wave touches 1 KB of each bf16 tensor
@@ -47,12 +47,6 @@ __device__ __forceinline__ Bf16x8 pack8(const float (&x)[8]) {
   return p;
 }
 
-// torch.nn.functional.softplus with beta = 1, threshold = 20.
-__device__ __forceinline__ float softplus20(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-
-// torch.nn.functional.logsigmoid: min(x, 0) - log1p(exp(-|x|)).
-__device__ __forceinline__ float logsigmoid(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }
-
 template <int LPR>
 __device__ __forceinline__ float row_sum(float v) {
 #pragma unroll
@@ -85,13 +79,13 @@ __global__ __launch_bounds__(kPrologueThreads) void prologue_kernel(PrologueArgs
   }
 
   // -exp(s_h) is computed once per head in fp32, then multiplies the softplus.
-  const float neg_rate = -expf(bf16_bits_to_f32(a.decay_scale_log[h]));
+  const float neg_rate = -gate_exp(bf16_bits_to_f32(a.decay_scale_log[h]));
   float g[8], sb[8], beta[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     g[i] = neg_rate * softplus20(f[i] + bias[i]);
-    sb[i] = bf16_to_f32((__bf16)expf(0.5f * logsigmoid(e[i])));
-    beta[i] = 1.f / (1.f + expf(-w[i]));
+    sb[i] = bf16_to_f32((__bf16)gate_exp(0.5f * logsigmoid(e[i])));
+    beta[i] = gate_sigmoid(w[i]);
   }
   const int64_t out = row * D + c0;
   float4* gp = (float4*)(a.g_out + out);

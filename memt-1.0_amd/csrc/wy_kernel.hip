@@ -52,8 +52,13 @@ __device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
   return r;
 }
 
-template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT>
+// RAW: the inputs are the memory block's projections (raw q, k, v, the decay
+// projection, erase and write logits); the kernel forms g, beta, q_hat and
+// k_til = sqrt_b * l2norm(k) itself, in the prologue's op order, and writes
+// q_hat for the snapshot read.
+template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT, bool RAW = false>
 __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
+  static_assert(!RAW || (!HAS_B && !G_CUM), "raw projections carry the erase gate in k and g un-summed");
   constexpr int C = kChunk;
   constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;
   constexpr int XP = C + 8;   // element pitch of the column-major xw / xu tiles
@@ -90,11 +95,55 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   // k / b / q for the per-channel loop), so each phase waits only for its own
   // inputs and the cumsum and factor phases run while the rest is in flight.
   // Rows past the chunk end read row 0 of the chunk and are zeroed where used.
-  bf16x8 kraw[KS], braw[HAS_B ? KS : 1], qraw[CAUSAL ? KS : 1];
+  constexpr bool WANT_Q = CAUSAL || RAW;
+  bf16x8 kraw[KS], braw[HAS_B ? KS : 1], qraw[WANT_Q ? KS : 1];
   float g[KS][8];
   using BetaRaw = typename std::conditional<sizeof(BetaT) == 4, f32x4, bf16x4>::type;
   bf16x4 vraw[VS][2];
   BetaRaw btraw[VS][2];
+  bf16x8 fraw[RAW ? KS : 1], fbias[RAW ? KS : 1], eraw[RAW ? KS : 1];
+  if constexpr (RAW) {
+    // projection rows: q, k, decay and erase rows H*K wide, v and write rows H*V
+    const size_t tr = (size_t)(tok0 + (valid ? t : 0));
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c0 = h * K + 32 * s + 16 * half + 4 * lg;
+        const bf16x4 ff = *(const bf16x4*)(a.f_raw + tr * a.f_stride + c0);
+        const bf16x4 bb = *(const bf16x4*)(a.decay_bias + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          fraw[s][4 * half + e] = ff[e];
+          fbias[s][4 * half + e] = bb[e];
+        }
+      }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < VS; ++s)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c0 = h * V + 32 * s + 16 * half + 4 * lg;
+        vraw[s][half] = *(const bf16x4*)(a.v + tr * a.v_stride + c0);
+        btraw[s][half] = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + c0);
+      }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c0 = h * K + 32 * s + 16 * half + 4 * lg;
+        const bf16x4 kk = *(const bf16x4*)(a.k + tr * a.k_stride + c0);
+        const bf16x4 ee = *(const bf16x4*)(a.e_raw + tr * a.e_stride + c0);
+        const bf16x4 qq = *(const bf16x4*)(a.q + tr * a.q_stride + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kraw[s][4 * half + e] = kk[e];
+          eraw[s][4 * half + e] = ee[e];
+          qraw[s][4 * half + e] = qq[e];
+        }
+      }
+  } else {
 #pragma unroll
   for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -129,6 +178,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
         if constexpr (CAUSAL) qraw[s][4 * half + e] = qq[e];
       }
     }
+  }
   auto kf = [&](int s, int j) { return (float)kraw[s][j]; };
   auto bkf = [&](int s, int j) { return HAS_B ? (float)kraw[s][j] * (float)braw[s][j] : (float)kraw[s][j]; };
   auto qf = [&](int s, int j) { return CAUSAL ? (float)qraw[s][j] : 0.f; };
@@ -139,7 +189,13 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   for (int s = 0; s < KS; ++s)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      g[s][j] = valid ? g[s][j] : 0.f;
+      if constexpr (RAW) {
+        // g = -exp(s_h) * softplus(f + bias): natural-log decay, fp32
+        const float neg_rate = -gate_exp((float)a.decay_scale_log[h]);
+        g[s][j] = valid ? neg_rate * softplus20((float)fraw[s][j] + (float)fbias[s][j]) : 0.f;
+      } else {
+        g[s][j] = valid ? g[s][j] : 0.f;
+      }
       gk[s][j] = G_CUM ? g[s][j] : row_inclusive_scan(g[s][j]);
     }
 #pragma unroll
@@ -226,7 +282,12 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     for (int half = 0; half < 2; ++half)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * (float)btraw[s][half][e] : 0.f);
+      {
+        // RAW: beta = bf16(sigmoid(write logit)), the reference's bf16 write gate
+        const float bt = RAW ? (float)(__bf16)gate_sigmoid((float)btraw[s][half][e])
+                             : (float)btraw[s][half][e];
+        xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * bt : 0.f);
+      }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int ct = 2 * s + half;
@@ -237,12 +298,51 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       *(f16x4*)(&xu_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
     }
   }
+  if constexpr (RAW) {
+    // q_hat = bf16(q / sqrt(sum q^2 + eps)), k_til = bf16(sqrt_b * bf16(k / sqrt(sum k^2 + eps)))
+    // with sqrt_b = bf16(exp(logsigmoid(e) / 2)); a token's channels sit on the four lanes lr + 16 i
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float qv = (float)qraw[s][j], kv = (float)kraw[s][j];
+        sq += qv * qv;
+        sk += kv * kv;
+      }
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    sk += __shfl_xor(sk, 16, 64);
+    sk += __shfl_xor(sk, 32, 64);
+    const float rq = 1.f / sqrtf(sq + a.eps), rk = 1.f / sqrtf(sk + a.eps);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sbv = (float)(__bf16)gate_exp(0.5f * logsigmoid((float)eraw[s][j]));
+        const float khat = (float)(__bf16)((float)kraw[s][j] * rk);
+        kraw[s][j] = (__bf16)(sbv * khat);
+        qraw[s][j] = (__bf16)((float)qraw[s][j] * rq);
+      }
+    if (valid && a.q_hat != nullptr) {
+      __bf16* qo = a.q_hat + ((size_t)(tok0 + t) * H + h) * K;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          bf16x4 o4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o4[e] = qraw[s][4 * half + e];
+          *(bf16x4*)(qo + 32 * s + 16 * half + 4 * lg) = o4;
+        }
+    }
+  }
   if (!valid) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       kraw[s] = bf16x8{};
       if constexpr (HAS_B) braw[s] = bf16x8{};
-      if constexpr (CAUSAL) qraw[s] = bf16x8{};
+      if constexpr (WANT_Q) qraw[s] = bf16x8{};
     }
   }
 
@@ -541,6 +641,13 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   }
 }
 
+template <int K, int V, bool CAUSAL>
+hipError_t launch_raw(const WyArgs& a, int n_chunk, hipStream_t stream) {
+  hipLaunchKernelGGL((wy_kernel<K, V, CAUSAL, false, false, __bf16, true>), dim3(n_chunk, a.H), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
 template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM>
 hipError_t launch_t(const WyArgs& a, int n_chunk, bool beta_bf16, hipStream_t stream) {
   dim3 grid(n_chunk, a.H), block(256);
@@ -554,6 +661,8 @@ hipError_t launch_t(const WyArgs& a, int n_chunk, bool beta_bf16, hipStream_t st
 template <int K, int V>
 hipError_t launch_kv(const WyArgs& a, int n_chunk, bool causal, bool g_cum, bool beta_bf16,
                      hipStream_t stream) {
+  if (a.f_raw != nullptr)
+    return causal ? launch_raw<K, V, true>(a, n_chunk, stream) : launch_raw<K, V, false>(a, n_chunk, stream);
   const bool has_b = a.b != nullptr;
 #define MEMT_WY_CASE(CA, HB, GC) \
   if (causal == CA && has_b == HB && g_cum == GC) return launch_t<K, V, CA, HB, GC>(a, n_chunk, beta_bf16, stream);

@@ -30,6 +30,8 @@ from .ops import (
     memory_prologue,
     read_slots,
     token_memory_packed_flash,
+    token_memory_packed_fused,
+    token_memory_packed_fused_slots,
     token_memory_packed_slots,
     workspace_bytes,
     write_gates,
@@ -66,4 +68,6 @@ __all__ = [
     "memory_prologue",
     "read_slots",
     "token_memory_packed_slots",
+    "token_memory_packed_fused",
+    "token_memory_packed_fused_slots",
 ]

@@ -33,7 +33,7 @@ OUT_CAUSAL = 2
 CHUNK_BLOCK_START = 1
 CHUNK_COMMIT = 2
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class Plan(ctypes.Structure):
@@ -70,6 +70,10 @@ _SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
     ),
+    "memt_gdn2_chunk_update_fused": (
+        _I,
+        [ctypes.c_void_p, _P, _P, _P, _P, _I, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
     "memt_gdn2_chunk_update_slots": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
@@ -91,6 +95,23 @@ _SIGNATURES = {
         [_P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I, _I, _F, _P],
     ),
 }
+
+class Projections(ctypes.Structure):
+    """``memt_gdn2_projections``: raw projection rows of the memory block."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_stride", ctypes.c_int64),
+        ("v", ctypes.c_void_p), ("v_stride", ctypes.c_int64),
+        ("decay", ctypes.c_void_p), ("decay_stride", ctypes.c_int64),
+        ("erase", ctypes.c_void_p), ("erase_stride", ctypes.c_int64),
+        ("write", ctypes.c_void_p), ("write_stride", ctypes.c_int64),
+        ("decay_bias", ctypes.c_void_p),
+        ("decay_scale_log", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
 
 _lib = None
 

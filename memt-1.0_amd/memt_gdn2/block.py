@@ -7,8 +7,10 @@ serving runtime makes per memory layer.  The dense projections stay torch
 GEMMs (hipBLASLt).  Everything after them runs in this package's kernels:
 
 * query samples: ``l2norm`` -> ``memt_gdn2_read_fwd`` -> ``MemTRMSNormGated``;
-* commit samples: one prologue kernel (gates, ``l2norm(q)``, ``sqrt_b * l2norm(k)``)
-  -> ``token_memory_packed`` -> ``MemTRMSNormGated``.
+* commit samples: the update with the gate and q/k prologue inside its WY
+  kernel (``fused_prologue=True``, the default), or one prologue kernel
+  (gates, ``l2norm(q)``, ``sqrt_b * l2norm(k)``) then ``token_memory_packed``;
+  then ``MemTRMSNormGated``.
 """
 
 from __future__ import annotations
@@ -22,15 +24,16 @@ from torch.nn import functional as F
 from .layout import WY_TILE_TOKENS, build_chunk_plan, validate_packed_inputs
 from .norm import MemTRMSNormGated
 from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, token_memory_packed,
-                  token_memory_packed_slots)
+                  token_memory_packed_fused, token_memory_packed_fused_slots, token_memory_packed_slots)
 
 
 class QwenMemoryBlock(nn.Module):
     """``memory_config`` needs ``hidden_size``, ``num_heads``, ``head_dim``,
     ``chunk_tokens``, ``rms_norm_eps`` and ``output_gate_softcap``."""
 
-    def __init__(self, memory_config, *, device=None):
+    def __init__(self, memory_config, *, device=None, fused_prologue: bool = True):
         super().__init__()
+        self.fused_prologue = fused_prologue
         hidden_size = memory_config.hidden_size
         num_heads = memory_config.num_heads
         head_dim = memory_config.head_dim
@@ -83,10 +86,16 @@ class QwenMemoryBlock(nn.Module):
         erase, write, decay_latent = torch.split(
             F.linear(hidden_batch, weight[self._write_gate_slice]), self.write_gate_rows, dim=-1)
         decay = self.f_down(decay_latent)
-        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H)
-        read, next_state = token_memory_packed(
-            q_hat, k_til, v.reshape(1, T, H, D), g, beta, read_states, write_states, erase=None, lengths=lengths,
-            scale=self.read_scale, chunk_tokens=self.chunk_tokens)
+        if self.fused_prologue:
+            read, next_state = token_memory_packed_fused(
+                q, k, v, decay, self.decay_bias, self.decay_scale_log, erase, write, read_states, write_states,
+                lengths=lengths, scale=self.read_scale, chunk_tokens=self.chunk_tokens, num_heads=H)
+        else:
+            q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write,
+                                                    H)
+            read, next_state = token_memory_packed(
+                q_hat, k_til, v.reshape(1, T, H, D), g, beta, read_states, write_states, erase=None,
+                lengths=lengths, scale=self.read_scale, chunk_tokens=self.chunk_tokens)
         output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
         return output.view(T, self.value_dim), next_state
 
@@ -117,10 +126,16 @@ class QwenMemoryBlock(nn.Module):
         erase, write, decay_latent = torch.split(
             F.linear(hidden_batch, weight[self._write_gate_slice]), self.write_gate_rows, dim=-1)
         decay = self.f_down(decay_latent)
-        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H)
-        read = token_memory_packed_slots(q_hat, k_til, v.reshape(1, T, H, D), g, beta, pool, read_slot, write_slot,
-                                         erase=None, lengths=lengths, scale=self.read_scale,
-                                         chunk_tokens=self.chunk_tokens)
+        if self.fused_prologue:
+            read = token_memory_packed_fused_slots(
+                q, k, v, decay, self.decay_bias, self.decay_scale_log, erase, write, pool, read_slot, write_slot,
+                lengths=lengths, scale=self.read_scale, chunk_tokens=self.chunk_tokens, num_heads=H)
+        else:
+            q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write,
+                                                    H)
+            read = token_memory_packed_slots(q_hat, k_til, v.reshape(1, T, H, D), g, beta, pool, read_slot,
+                                             write_slot, erase=None, lengths=lengths, scale=self.read_scale,
+                                             chunk_tokens=self.chunk_tokens)
         output = self.o_norm(read.reshape(-1, D), output_gate.reshape(-1, D))
         return output.view(T, self.value_dim)
 

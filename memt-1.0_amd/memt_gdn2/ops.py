@@ -34,6 +34,8 @@ __all__ = [
     "memory_prologue",
     "token_memory_packed_slots",
     "read_slots",
+    "token_memory_packed_fused",
+    "token_memory_packed_fused_slots",
 ]
 
 _DT = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
@@ -600,3 +602,102 @@ def read_slots(q, pool, read_slots_, lengths, scale):
         "read_fwd_slots",
     )
     return out
+
+
+# ---------------------------------------------------------------------------
+# The commit path from raw projections (prologue inside the WY kernel)
+# ---------------------------------------------------------------------------
+
+
+def _raw_rows(x: torch.Tensor, width: int, name: str):
+    """``x`` as ``[T, width]`` bf16 rows read in place (row stride a multiple of 4
+    elements, 8-byte aligned); anything else is made contiguous first."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bf16")
+    if x.shape[-1] != width:
+        raise ValueError(f"{name} must have {width} channels per token, got {tuple(x.shape)}")
+    try:
+        x2 = x.view(-1, width)
+    except RuntimeError:
+        x2 = x.reshape(-1, width).contiguous()
+    if x2.stride(1) != 1 or x2.stride(0) % 4 or x2.data_ptr() % 8 or (x2.shape[0] > 1 and x2.stride(0) < width):
+        x2 = x2.contiguous()
+    return x2, (x2.stride(0) if x2.shape[0] > 1 else width)
+
+
+def _fused_update(q, k, v, decay, decay_bias, decay_scale_log, erase, write, num_heads, *, plan, scale, eps,
+                  h0, ht, read_states, slots=None, n_slots=0):
+    lib = _lib.load()
+    _lib.require_gpu(q, k, v, decay, erase, write)
+    H = num_heads
+    K = k.shape[-1] // H
+    V = v.shape[-1] // H
+    rows = {}
+    for name, t, wdt in (("q", q, H * K), ("k", k, H * K), ("v", v, H * V), ("decay", decay, H * K),
+                         ("erase", erase, H * K), ("write", write, H * V)):
+        rows[name] = _raw_rows(t, wdt, name)
+    T = rows["k"][0].shape[0]
+    if any(r[0].shape[0] != T for r in rows.values()) or plan.total_tokens != T:
+        raise ValueError("projections and plan must cover the same tokens")
+    bias, rate = _gate_params(decay_bias, decay_scale_log, H, K, k.device)
+    x = _lib.Projections(
+        q=rows["q"][0].data_ptr(), q_stride=rows["q"][1], k=rows["k"][0].data_ptr(), k_stride=rows["k"][1],
+        v=rows["v"][0].data_ptr(), v_stride=rows["v"][1], decay=rows["decay"][0].data_ptr(),
+        decay_stride=rows["decay"][1], erase=rows["erase"][0].data_ptr(), erase_stride=rows["erase"][1],
+        write=rows["write"][0].data_ptr(), write_stride=rows["write"][1], decay_bias=bias.data_ptr(),
+        decay_scale_log=rate.data_ptr(), eps=float(eps), reserved=0)
+    dev = k.device
+    q_hat = torch.empty(1, T, H, K, dtype=torch.bfloat16, device=dev)
+    o = torch.empty(1, T, H, V, dtype=torch.bfloat16, device=dev)
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "snapshot", plan.num_sample))
+    p = plan.abi()
+    rs, s0, s1 = slots if slots is not None else (None, None, None)
+    _lib.check(
+        lib.memt_gdn2_chunk_update_fused(
+            ctypes.addressof(x), q_hat.data_ptr(), _lib.ptr(h0), _lib.ptr(ht), _lib.ptr(read_states), n_slots,
+            _lib.ptr(rs), _lib.ptr(s0), _lib.ptr(s1), o.data_ptr(), ctypes.byref(p), T, H, K, V, float(scale),
+            _OUT["snapshot"], ws.data_ptr(), ws.numel(), _lib.stream_of(dev)),
+        "chunk_update_fused",
+    )
+    return o
+
+
+def token_memory_packed_fused(q, k, v, decay, decay_bias, decay_scale_log, erase, write, read_states, write_states, *,
+                              lengths, scale, chunk_tokens, num_heads, eps: float = 1e-6):
+    """The commit path of ``QwenMemoryBlock.packed`` (models/qwen/layer.py:132-150)
+    from its raw projections: ``q, k, decay, erase`` ``[T, H*K]``, ``v, write``
+    ``[T, H*V]`` bf16 (views of the projection outputs are read in place),
+    ``decay_bias`` ``[H*K]``, ``decay_scale_log`` ``[H]``.  The gate and q/k
+    prologue runs inside the update.  Returns ``(read [1,T,H,V] bf16,
+    final [N,H,K,V] fp32)`` as ``token_memory_packed`` of the prologue's outputs."""
+    if not lengths or any(int(n) <= 0 for n in lengths):
+        raise ValueError("Packed sample lengths must be positive")
+    H = num_heads
+    K, V = k.shape[-1] // H, v.shape[-1] // H
+    plan = packed_plan(lengths, k.device, chunk_tokens=chunk_tokens)
+    expected = (plan.num_sample, H, K, V)
+    for name, t in (("write_states", write_states), ("read_states", read_states)):
+        if tuple(t.shape) != expected or t.dtype != torch.float32 or not t.is_cuda:
+            raise ValueError(f"{name} must be fp32 {expected} on the GPU")
+    h0, rs = _contig(write_states, read_states)
+    final = torch.empty(expected, dtype=torch.float32, device=k.device)
+    o = _fused_update(q, k, v, decay, decay_bias, decay_scale_log, erase, write, H, plan=plan, scale=scale, eps=eps,
+                      h0=h0, ht=final, read_states=rs)
+    return o, final
+
+
+def token_memory_packed_fused_slots(q, k, v, decay, decay_bias, decay_scale_log, erase, write, pool, read_slots,
+                                    write_slots, *, lengths, scale, chunk_tokens, num_heads, eps: float = 1e-6):
+    """``token_memory_packed_fused`` on a state pool in place, as
+    ``token_memory_packed_slots``.  Returns ``read``."""
+    if not lengths or any(int(n) <= 0 for n in lengths):
+        raise ValueError("Packed sample lengths must be positive")
+    H = num_heads
+    K, V = k.shape[-1] // H, v.shape[-1] // H
+    pv = _pool_view(pool, H, K, V)
+    plan = packed_plan(lengths, k.device, chunk_tokens=chunk_tokens)
+    N = plan.num_sample
+    rs = _slot_index(read_slots, N, pv.shape[0], k.device, "read_slots")
+    ws_ = _slot_index(write_slots, N, pv.shape[0], k.device, "write_slots", distinct=True)
+    return _fused_update(q, k, v, decay, decay_bias, decay_scale_log, erase, write, H, plan=plan, scale=scale,
+                         eps=eps, h0=pv, ht=pv, read_states=pv, slots=(rs, ws_, ws_), n_slots=pv.shape[0])

@@ -147,11 +147,13 @@ def _oracle_packed(block, hidden, read_states, lengths, commit, write_states):
     return out.reshape(T, W), final
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("commit", [False, True])
-def test_block_packed(dev, commit):
-    print(f"block packed commit={commit}", flush=True)
+def test_block_packed(dev, commit, fused):
+    print(f"block packed commit={commit} fused={fused}", flush=True)
     cfg = _config()
     block = _block(dev, cfg)
+    block.fused_prologue = fused
     lengths = [150, 1, 300]
     T = sum(lengths)
     g = torch.Generator().manual_seed(5)
@@ -198,3 +200,45 @@ def test_runtime_step_on_gpu_slots(dev):
     assert torch.equal(out[0:70], rc[:70]) and torch.equal(out[76:96], rc[70:])
     assert torch.equal(pool.storage[0][4, 0], fc[0]) and torch.equal(pool.storage[0][5, 0], fc[1])
     assert torch.equal(pool.storage[0][:4], before[:4])
+
+
+@pytest.mark.parametrize("D,lengths", [(128, [150, 1, 300]), (64, [40, 700]), (256, [90, 130])])
+def test_fused_prologue_update(dev, D, lengths):
+    """The update from raw projections (prologue in the WY kernel) against the
+    prologue kernel followed by token_memory_packed, and against the oracle;
+    the slot form on the same inputs gives the same bits."""
+    print(f"fused prologue D={D} lengths={lengths}", flush=True)
+    H = 2
+    T = sum(lengths)
+    q, k, decay, bias, rate, erase, write = _fused_rows(T, H, D, dev, seed=40 + D)
+    v = (torch.randn(T, 3 * H * D, device=dev) * 1.0).to(torch.bfloat16)[:, 2 * H * D:]
+    gen = torch.Generator(device=dev).manual_seed(41)
+    rs = torch.randn(len(lengths), H, D, D, generator=gen, device=dev) * 0.05
+    ws = torch.randn(len(lengths), H, D, D, generator=gen, device=dev) * 0.05
+    read, final = memt_gdn2.token_memory_packed_fused(q, k, v, decay, bias, rate, erase, write, rs, ws,
+                                                      lengths=lengths, scale=D ** -0.5, chunk_tokens=256,
+                                                      num_heads=H)
+    q_hat, k_til, beta, g = memt_gdn2.memory_prologue(q, k, decay, bias, rate, erase, write, H)
+    read2, final2 = memt_gdn2.token_memory_packed(q_hat, k_til, v.reshape(1, T, H, D), g, beta, rs, ws, erase=None,
+                                                  lengths=lengths, scale=D ** -0.5, chunk_tokens=256)
+    assert O.parity_err(host(read), host(read2), out_bf16=True) <= 1e-3
+    assert O.max_rel_err(host(final), host(final2)) <= 1e-3
+    # the oracle from the same projections
+    g_ref, sb_ref, beta_ref = _ref_gates(decay, bias, rate, erase, write, H)
+    qh = O.l2norm(host(q).reshape(1, T, H, D), 1e-6, out_bf16=True)[0]
+    kt = O.bf16_round(sb_ref.reshape(1, T, H, D) * O.l2norm(host(k).reshape(1, T, H, D), 1e-6, out_bf16=True)[0])
+    r_ref, f_ref = O.token_memory_packed(qh, kt, host(v).reshape(1, T, H, D), g_ref.reshape(1, T, H, D),
+                                         beta_ref.reshape(1, T, H, D), host(rs), host(ws), erase=None,
+                                         lengths=lengths, scale=D ** -0.5, chunk_tokens=256)
+    assert O.max_rel_err(host(final), f_ref) <= TOL
+    assert O.parity_err(host(read), r_ref, out_bf16=True) <= TOL
+    pool = torch.zeros(len(lengths) + 3, H, D, D, device=dev)
+    slots_w = [len(lengths) + 2 - i for i in range(len(lengths))]
+    slots_r = list(range(len(lengths)))
+    pool[slots_w] = ws
+    pool[slots_r] = rs
+    read3 = memt_gdn2.token_memory_packed_fused_slots(q, k, v, decay, bias, rate, erase, write, pool, slots_r,
+                                                      slots_w, lengths=lengths, scale=D ** -0.5, chunk_tokens=256,
+                                                      num_heads=H)
+    torch.cuda.synchronize()
+    assert torch.equal(read3, read) and torch.equal(pool[slots_w], final)
