@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int un
     scan_body<K, V, NSV, false, 2>(a, r / a.H, r % a.H, NSV * slice, S_lds, Vn_lds);
 }
 
-// Phase 2 of the two-level scan, one workgroup per (sequence, head, 32 state
+// Phase 2 of the two-level scan, one workgroup per (sequence, head, 16 state
 // columns): S_{g+1} = P_g S_g + Q_g over the sequence's groups, writing the state
 // entering every group but the first.  P_g S_g is split-bf16 MFMA
 // (P_hi S_hi + P_hi S_lo + P_lo S_hi) with fp32 accumulation; P and Q of the
@@ -471,13 +471,13 @@ template <int K, int V>
 struct CombineFrag {
   static constexpr int RT = K / 64, KS = K / 32;
   bf16x8 ph[RT][KS], pl[RT][KS];
-  f32x4 q[RT][2];
+  f32x4 q[RT][1];
 };
 
 template <int K, int V>
 __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
   using F = CombineFrag<K, V>;
-  constexpr int BV = 32, NV = V / BV, RT = F::RT, KS = F::KS, CT = 2, SP = K + kSPad;
+  constexpr int BV = 16, NV = V / BV, RT = F::RT, KS = F::KS, CT = 1, SP = K + kSPad;
   __shared__ __attribute__((aligned(16))) __bf16 Shi[BV * SP];
   __shared__ __attribute__((aligned(16))) __bf16 Slo[BV * SP];
   const int H = a.H;
@@ -613,7 +613,7 @@ hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
     units = group_bound(a.n_chunk, a.n_seq, a.group_L);
     const int nt = units * a.H * (K / scan_slice(K) + V / scan_slice(V));
     hipLaunchKernelGGL((trans_kernel<K, V>), dim3(nt), dim3(kScanThreads), 0, stream, a, units);
-    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 32) * a.H * a.n_seq), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 16) * a.H * a.n_seq), dim3(256), 0, stream, a);
   }
   const dim3 grid(units * a.H * (V / scan_slice(V))), block(kScanThreads);
   if (causal)

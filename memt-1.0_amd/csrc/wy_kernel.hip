@@ -408,10 +408,8 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + c0]);
       const f32x4 gw = *(const f32x4*)(&fac_s[(7 + wave) * K + c0]);
       const f32x4 ew = *(const f32x4*)(&fac_s[(11 + wave) * K + c0]);
-      const f32x4 lastv = *(const f32x4*)(&fac_s[15 * K + c0]);
       const int wn = wave < 3 ? wave : 2;
       const f32x4 dj = *(const f32x4*)(&fac_s[(4 + wn) * K + c0]);
-      const f32x4 rn = *(const f32x4*)(&fac_s[(wn + 1) * K + c0]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int j = 4 * half + e;
@@ -423,13 +421,30 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
         xw8[s][j] = (_Float16)(av * ew[e]);
         const float kbv = kf(s, j) * ifa;
         kbs[j] = kbv;
-        kg8[j] = (_Float16)(wide ? kf(s, j) * fast_exp2(lastv[e] - gk[s][j]) : kbv * gw[e]);
-        base[j] = kf(s, j) * (wide ? fast_exp2(rn[e] - gk[s][j]) : ifa * dj[e]);
+        kg8[j] = (_Float16)(kbv * gw[e]);
+        base[j] = kbv * dj[e];
         if constexpr (CAUSAL) {
           const float qv = qf(s, j) * fa;
           qvs[j] = qv;
           aq16[s][j] = (_Float16)qv;
           qg8[j] = (_Float16)(qv * ew[e]);
+        }
+      }
+    }
+    if (wide) {
+      // exact factors where the re-centred ones could overflow (a scalar branch,
+      // so their exp2s run only for such blocks)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c0 = 32 * s + 16 * half + 4 * lg;
+        const f32x4 lastv = *(const f32x4*)(&fac_s[15 * K + c0]);
+        const int wn = wave < 3 ? wave : 2;
+        const f32x4 rn = *(const f32x4*)(&fac_s[(wn + 1) * K + c0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * half + e;
+          kg8[j] = (_Float16)(kf(s, j) * fast_exp2(lastv[e] - gk[s][j]));
+          base[j] = kf(s, j) * fast_exp2(rn[e] - gk[s][j]);
         }
       }
     }
