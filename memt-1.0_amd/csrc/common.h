@@ -61,6 +61,20 @@ __device__ __forceinline__ float softplus20(float x) {
 // torch.nn.functional.logsigmoid: min(x, 0) - log1p(e^-|x|)
 __device__ __forceinline__ float logsigmoid(float x) { return fminf(x, 0.f) - gate_log1p(gate_exp(-fabsf(x))); }
 __device__ __forceinline__ float gate_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + gate_exp(-x)); }
+// Gates whose results are stored as bf16 (beta, sqrt_b) need only ~1e-6
+// relative accuracy, far below a bf16 ulp (2^-8): the plain 2^(x log2 e).
+__device__ __forceinline__ float sigmoid_bf16(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.44269502f));
+}
+// softplus for a decay that only feeds the in-kernel cumsum: max(x, 0) +
+// ln2 * log2(1 + 2^(-|x| log2 e)), absolute error ~1e-7 (the decay factors it
+// yields move by ~1e-5 relative over a 64-token chunk)
+__device__ __forceinline__ float softplus_internal(float x) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(x) * 1.44269502f);
+  return fmaxf(x, 0.f) + __builtin_amdgcn_logf(1.f + y) * 0.693147182f;
+}
+// sqrt_b = exp(logsigmoid(e) / 2), computed as sqrt(sigmoid(e)) (the same value)
+__device__ __forceinline__ float sqrt_sigmoid_bf16(float x) { return __builtin_sqrtf(sigmoid_bf16(x)); }
 
 __device__ __forceinline__ float bf16_to_f32(__bf16 x) { return (float)x; }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }

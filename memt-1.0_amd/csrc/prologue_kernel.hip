@@ -84,8 +84,8 @@ __global__ __launch_bounds__(kPrologueThreads) void prologue_kernel(PrologueArgs
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     g[i] = neg_rate * softplus20(f[i] + bias[i]);
-    sb[i] = bf16_to_f32((__bf16)gate_exp(0.5f * logsigmoid(e[i])));
-    beta[i] = gate_sigmoid(w[i]);
+    sb[i] = bf16_to_f32((__bf16)sqrt_sigmoid_bf16(e[i]));
+    beta[i] = sigmoid_bf16(w[i]);
   }
   const int64_t out = row * D + c0;
   float4* gp = (float4*)(a.g_out + out);

@@ -184,6 +184,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   auto qf = [&](int s, int j) { return CAUSAL ? (float)qraw[s][j] : 0.f; };
 
   // ---- cumsum: inclusive within the 16-token block, then block offsets ----
+  const float neg_rate = RAW ? -gate_exp((float)a.decay_scale_log[h]) : 0.f;  // -exp(s_h), uniform
   float gk[KS][8];
 #pragma unroll
   for (int s = 0; s < KS; ++s)
@@ -191,8 +192,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     for (int j = 0; j < 8; ++j) {
       if constexpr (RAW) {
         // g = -exp(s_h) * softplus(f + bias): natural-log decay, fp32
-        const float neg_rate = -gate_exp((float)a.decay_scale_log[h]);
-        g[s][j] = valid ? neg_rate * softplus20((float)fraw[s][j] + (float)fbias[s][j]) : 0.f;
+        g[s][j] = valid ? neg_rate * softplus_internal((float)fraw[s][j] + (float)fbias[s][j]) : 0.f;
       } else {
         g[s][j] = valid ? g[s][j] : 0.f;
       }
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       for (int e = 0; e < 4; ++e)
       {
         // RAW: beta = bf16(sigmoid(write logit)), the reference's bf16 write gate
-        const float bt = RAW ? (float)(__bf16)gate_sigmoid((float)btraw[s][half][e])
+        const float bt = RAW ? (float)(__bf16)sigmoid_bf16((float)btraw[s][half][e])
                              : (float)btraw[s][half][e];
         xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * bt : 0.f);
       }
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float sbv = (float)(__bf16)gate_exp(0.5f * logsigmoid((float)eraw[s][j]));
+        const float sbv = (float)(__bf16)sqrt_sigmoid_bf16((float)eraw[s][j]);
         const float khat = (float)(__bf16)((float)kraw[s][j] * rk);
         kraw[s][j] = (__bf16)(sbv * khat);
         qraw[s][j] = (__bf16)((float)qraw[s][j] * rq);
