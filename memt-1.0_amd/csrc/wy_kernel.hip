@@ -52,15 +52,22 @@ __device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
   return r;
 }
 
+// Channel groups of 4 waves: the K channels (and V value columns) split into
+// NCG groups, each handled by its own 4 waves with the d = 128 register plan;
+// the L / Aqk tiles are summed over the groups through LDS.
+__host__ __device__ constexpr int wy_groups(int K) { return K >= 256 ? 2 : 1; }
+
 // RAW: the inputs are the memory block's projections (raw q, k, v, the decay
 // projection, erase and write logits); the kernel forms g, beta, q_hat and
 // k_til = sqrt_b * l2norm(k) itself, in the prologue's op order, and writes
 // q_hat for the snapshot read.
 template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT, bool RAW = false>
-__global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
+__global__ __launch_bounds__(256 * wy_groups(K), K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   static_assert(!RAW || (!HAS_B && !G_CUM), "raw projections carry the erase gate in k and g un-summed");
   constexpr int C = kChunk;
-  constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;
+  constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;  // whole-head counts (record layouts)
+  constexpr int NCG = wy_groups(K), NT = 256 * NCG;
+  constexpr int KSL = KS / NCG, VSL = VS / NCG, KTL = KT / NCG, VTL = VT / NCG;  // per channel group
   constexpr int XP = C + 8;   // element pitch of the column-major xw / xu tiles
   constexpr int AP = C + 4;   // fp32 pitch of As_s
   constexpr int LQ = 16 + 4;  // fp32 pitch of a diagonal L tile
@@ -79,10 +86,14 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   __shared__ __attribute__((aligned(16))) float As_s[C * AP];     // A, row-major
   __shared__ __attribute__((aligned(16))) float Ld_s[4 * 16 * LQ];
   _Float16* const xw_s = xch_s;
+  __shared__ float nrm_s[RAW && NCG > 1 ? 2 * NCG * C : 1];  // per-group l2norm sums
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);  // token block; uniform: scalar branches
+  const int cg = __builtin_amdgcn_readfirstlane(tid >> 8);          // channel group
+  const int cb = cg * (K / NCG), vcb = cg * (V / NCG);             // its first channel / value column
+  const int sg0 = cg * KSL, vg0 = cg * VSL;                         // its first channel / value step
   const int tok0 = a.chunk_tok0[chunk], len = a.chunk_len[chunk];
   const size_t unit = (size_t)chunk * H + h;
   const int t = 16 * wave + lr;
@@ -96,20 +107,20 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   // inputs and the cumsum and factor phases run while the rest is in flight.
   // Rows past the chunk end read row 0 of the chunk and are zeroed where used.
   constexpr bool WANT_Q = CAUSAL || RAW;
-  bf16x8 kraw[KS], braw[HAS_B ? KS : 1], qraw[WANT_Q ? KS : 1];
-  float g[KS][8];
+  bf16x8 kraw[KSL], braw[HAS_B ? KSL : 1], qraw[WANT_Q ? KSL : 1];
+  float g[KSL][8];
   using BetaRaw = typename std::conditional<sizeof(BetaT) == 4, f32x4, bf16x4>::type;
-  bf16x4 vraw[VS][2];
-  BetaRaw btraw[VS][2];
-  bf16x8 fraw[RAW ? KS : 1], fbias[RAW ? KS : 1], eraw[RAW ? KS : 1];
+  bf16x4 vraw[VSL][2];
+  BetaRaw btraw[VSL][2];
+  bf16x8 fraw[RAW ? KSL : 1], fbias[RAW ? KSL : 1], eraw[RAW ? KSL : 1];
   if constexpr (RAW) {
     // projection rows: q, k, decay and erase rows H*K wide, v and write rows H*V
     const size_t tr = (size_t)(tok0 + (valid ? t : 0));
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = h * K + 32 * s + 16 * half + 4 * lg;
+        const int c0 = h * K + cb + 32 * s + 16 * half + 4 * lg;
         const bf16x4 ff = *(const bf16x4*)(a.f_raw + tr * a.f_stride + c0);
         const bf16x4 bb = *(const bf16x4*)(a.decay_bias + c0);
 #pragma unroll
@@ -120,19 +131,19 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int s = 0; s < VS; ++s)
+    for (int s = 0; s < VSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = h * V + 32 * s + 16 * half + 4 * lg;
+        const int c0 = h * V + vcb + 32 * s + 16 * half + 4 * lg;
         vraw[s][half] = *(const bf16x4*)(a.v + tr * a.v_stride + c0);
         btraw[s][half] = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + c0);
       }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = h * K + 32 * s + 16 * half + 4 * lg;
+        const int c0 = h * K + cb + 32 * s + 16 * half + 4 * lg;
         const bf16x4 kk = *(const bf16x4*)(a.k + tr * a.k_stride + c0);
         const bf16x4 ee = *(const bf16x4*)(a.e_raw + tr * a.e_stride + c0);
         const bf16x4 qq = *(const bf16x4*)(a.q + tr * a.q_stride + c0);
@@ -145,28 +156,28 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       }
   } else {
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const f32x4 gg = *(const f32x4*)(a.g + rowK + 32 * s + 16 * half + 4 * lg);
+      const f32x4 gg = *(const f32x4*)(a.g + rowK + cb + 32 * s + 16 * half + 4 * lg);
 #pragma unroll
       for (int e = 0; e < 4; ++e) g[s][4 * half + e] = gg[e];
     }
   asm volatile("" ::: "memory");
 #pragma unroll
-  for (int s = 0; s < VS; ++s)
+  for (int s = 0; s < VSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
       vraw[s][half] = *(const bf16x4*)(a.v + rowV + c0);
       btraw[s][half] = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
     }
   asm volatile("" ::: "memory");
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const int c0 = cb + 32 * s + 16 * half + 4 * lg;
       const bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
       bf16x4 bb{}, qq{};
       if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
@@ -185,9 +196,9 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
 
   // ---- cumsum: inclusive within the 16-token block, then block offsets ----
   const float neg_rate = RAW ? -gate_exp((float)a.decay_scale_log[h]) : 0.f;  // -exp(s_h), uniform
-  float gk[KS][8];
+  float gk[KSL][8];
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (RAW) {
@@ -199,10 +210,10 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       gk[s][j] = G_CUM ? g[s][j] : row_inclusive_scan(g[s][j]);
     }
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const int c0 = cb + 32 * s + 16 * half + 4 * lg;
       const f32x4 gkv{gk[s][4 * half], gk[s][4 * half + 1], gk[s][4 * half + 2], gk[s][4 * half + 3]};
       const f32x4 gv{g[s][4 * half], g[s][4 * half + 1], g[s][4 * half + 2], g[s][4 * half + 3]};
       if (!G_CUM && lr == 15) *(f32x4*)(&tot_s[wave * K + c0]) = gkv;
@@ -211,10 +222,10 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     }
   lds_barrier();
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const int c0 = cb + 32 * s + 16 * half + 4 * lg;
       if constexpr (!G_CUM) {
         f32x4 base = zero4();
         for (int w2 = 0; w2 < wave; ++w2) base += *(const f32x4*)(&tot_s[w2 * K + c0]);
@@ -226,7 +237,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
         for (int e = 0; e < 4; ++e) gk[s][4 * half + e] = lv[e];
       }
     }
-  for (int idx = tid; idx < 2 * K; idx += 256) {
+  for (int idx = tid; idx < 2 * K; idx += NT) {
     // two threads per channel: part 0 writes the block starts, their ratios and gk_last,
     // part 1 the powers used by kg and by xw / qg
     const int c = idx % K, part = idx / K;
@@ -276,7 +287,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     }
   // beta v to LDS, column-major (channel rows, token columns); read by the U product
 #pragma unroll
-  for (int s = 0; s < VS; ++s) {
+  for (int s = 0; s < VSL; ++s) {
     f16x8 xu8;
 #pragma unroll
     for (int half = 0; half < 2; ++half)
@@ -290,7 +301,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int ct = 2 * s + half;
+      const int ct = 2 * (vg0 + s) + half;
       const f32x4 tr = mfma_f16(xu8, sel_h[half], zero4());
       f16x4 o4;
 #pragma unroll
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     // with sqrt_b = bf16(exp(logsigmoid(e) / 2)); a token's channels sit on the four lanes lr + 16 i
     float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float qv = (float)qraw[s][j], kv = (float)kraw[s][j];
@@ -314,9 +325,23 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     sq += __shfl_xor(sq, 32, 64);
     sk += __shfl_xor(sk, 16, 64);
     sk += __shfl_xor(sk, 32, 64);
+    if constexpr (NCG > 1) {
+      // each group holds K / NCG of the token's channels
+      if (lg == 0) {
+        nrm_s[(cg * C + t) * 2] = sq;
+        nrm_s[(cg * C + t) * 2 + 1] = sk;
+      }
+      lds_barrier();
+      sq = sk = 0.f;
+#pragma unroll
+      for (int c2 = 0; c2 < NCG; ++c2) {
+        sq += nrm_s[(c2 * C + t) * 2];
+        sk += nrm_s[(c2 * C + t) * 2 + 1];
+      }
+    }
     const float rq = 1.f / sqrtf(sq + a.eps), rk = 1.f / sqrtf(sk + a.eps);
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float sbv = (float)(__bf16)sqrt_sigmoid_bf16((float)eraw[s][j]);
@@ -327,19 +352,19 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     if (valid && a.q_hat != nullptr) {
       __bf16* qo = a.q_hat + ((size_t)(tok0 + t) * H + h) * K;
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+      for (int s = 0; s < KSL; ++s)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           bf16x4 o4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) o4[e] = qraw[s][4 * half + e];
-          *(bf16x4*)(qo + 32 * s + 16 * half + 4 * lg) = o4;
+          *(bf16x4*)(qo + cb + 32 * s + 16 * half + 4 * lg) = o4;
         }
     }
   }
   if (!valid) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
+    for (int s = 0; s < KSL; ++s) {
       kraw[s] = bf16x8{};
       if constexpr (HAS_B) braw[s] = bf16x8{};
       if constexpr (WANT_Q) qraw[s] = bf16x8{};
@@ -349,10 +374,10 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   // ---- in-block decay span: a wide block takes exact diagonal products ----
   float span = 0.f;
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
+  for (int s = 0; s < KSL; ++s)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + 32 * s + 16 * half + 4 * lg]);
+      const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + cb + 32 * s + 16 * half + 4 * lg]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) span = fmaxf(span, r4[e] - gk[s][4 * half + e]);
     }
@@ -365,7 +390,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) pl[j] = pq[j] = 0.f;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+    for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
 #pragma unroll
@@ -394,17 +419,17 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   // Off-diagonal column operands are built by wave J for row blocks I > J:
   // k 2^(start_I - gk) = k (1/fa) prod_{w=J}^{I-1} 2^(start_{w+1} - start_w), each factor <= 1.
   auto pair_index = [](int I, int J) { return J * (7 - J) / 2 + (I - J - 1); };
-  f16x8 a16[KS], aq16[CAUSAL ? KS : 1];
-  f16x8 xw8[KS];
+  f16x8 a16[KSL], aq16[CAUSAL ? KSL : 1];
+  f16x8 xw8[KSL];
   _Float16* const kg_out = a.out.kgT + unit * (size_t)(C * K);
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  for (int s = 0; s < KSL; ++s) {
     f16x8 qg8, kg8;
     float avs[8], kbs[8], qvs[8];
     float base[8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int c0 = 32 * s + 16 * half + 4 * lg;
+      const int c0 = cb + 32 * s + 16 * half + 4 * lg;
       const f32x4 r4 = *(const f32x4*)(&fac_s[wave * K + c0]);
       const f32x4 gw = *(const f32x4*)(&fac_s[(7 + wave) * K + c0]);
       const f32x4 ew = *(const f32x4*)(&fac_s[(11 + wave) * K + c0]);
@@ -436,7 +461,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       // so their exp2s run only for such blocks)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = 32 * s + 16 * half + 4 * lg;
+        const int c0 = cb + 32 * s + 16 * half + 4 * lg;
         const f32x4 lastv = *(const f32x4*)(&fac_s[15 * K + c0]);
         const int wn = wave < 3 ? wave : 2;
         const f32x4 rn = *(const f32x4*)(&fac_s[(wn + 1) * K + c0]);
@@ -457,11 +482,11 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
       }
     }
     if constexpr (CAUSAL)
-      *(f16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + s) * 64 + lane) * 8) = qg8;
+      *(f16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + sg0 + s) * 64 + lane) * 8) = qg8;
     // kg^T to global as P-frags (rows = channels, reduction = tokens)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const int ct = 2 * s + half;
+      const int ct = 2 * (sg0 + s) + half;
       const f32x4 tr = mfma_f16(kg8, sel_h[half], zero4());
       f16x4 o4;
 #pragma unroll
@@ -475,7 +500,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
         if (I > wave + 1) {
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
-            const f32x4 dn = *(const f32x4*)(&fac_s[(4 + I - 1) * K + 32 * s + 16 * half + 4 * lg]);
+            const f32x4 dn = *(const f32x4*)(&fac_s[(4 + I - 1) * K + cb + 32 * s + 16 * half + 4 * lg]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) base[4 * half + e] *= dn[e];
           }
@@ -483,7 +508,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
         f16x8 op;
 #pragma unroll
         for (int j = 0; j < 8; ++j) op[j] = (_Float16)base[j];
-        *(f16x8*)(&xch_s[((size_t)(pair_index(I, wave) * KS + s) * 64 + lane) * 8]) = op;
+        *(f16x8*)(&xch_s[((size_t)(pair_index(I, wave) * KS + sg0 + s) * 64 + lane) * 8]) = op;
       }
     }
   }
@@ -500,12 +525,41 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   for (int J = 0; J < 3; ++J) {
     if (J >= wave) continue;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const f16x8 op = *(const f16x8*)(&xch_s[((size_t)(pair_index(wave, J) * KS + s) * 64 + lane) * 8]);
+    for (int s = 0; s < KSL; ++s) {
+      const f16x8 op = *(const f16x8*)(&xch_s[((size_t)(pair_index(wave, J) * KS + sg0 + s) * 64 + lane) * 8]);
       Lt[J] = mfma_f16(op, a16[s], Lt[J]);
       if constexpr (CAUSAL) Qt[J] = mfma_f16(op, aq16[s], Qt[J]);
     }
   }
+  if constexpr (NCG > 1) {
+    // sum the groups' partial tiles into group 0 (tiles J <= wave: 10 per group
+    // and matrix), through the off-diagonal operand buffer, dead once read
+    lds_barrier();
+    float* red = (float*)xch_s;
+    auto slot = [&](int g2, int q2, int J) { return ((((g2 - 1) * 2 + q2) * 10 + wave * (wave + 1) / 2 + J) * 64 + lane) * 4; };
+    if (cg > 0) {
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        if (J > wave) continue;
+        *(f32x4*)(&red[slot(cg, 0, J)]) = Lt[J];
+        if constexpr (CAUSAL) *(f32x4*)(&red[slot(cg, 1, J)]) = Qt[J];
+      }
+    }
+    lds_barrier();
+    if (cg == 0) {
+#pragma unroll
+      for (int g2 = 1; g2 < NCG; ++g2)
+#pragma unroll
+        for (int J = 0; J < 4; ++J) {
+          if (J > wave) continue;
+          Lt[J] += *(const f32x4*)(&red[slot(g2, 0, J)]);
+          if constexpr (CAUSAL) Qt[J] += *(const f32x4*)(&red[slot(g2, 1, J)]);
+        }
+    }
+  }
+  // masks, the Aqk record, the inverse: group 0 (the other groups wait at the barriers)
+  f32x4 Aii = zero4();
+  if (cg == 0) {
   // masks: L strictly lower, Aqk lower with the diagonal, scaled
 #pragma unroll
   for (int J = 0; J < 4; ++J) {
@@ -529,7 +583,6 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
   }
 
   // ---- A_II by row substitution: x (I + L_II) = e_lr, x[m] = d_lm - sum_{p>m} x[p] L[p][m] ----
-  f32x4 Aii;
   {
     float* Ld = Ld_s + wave * 16 * LQ;
     f32x4 ld4 = zero4();
@@ -560,22 +613,23 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
 #pragma unroll
   for (int J = 0; J < 4; ++J)
     if (J > wave) *(f32x4*)(&As_s[(16 * wave + lr) * AP + 16 * J + 4 * lg]) = zero4();
+  }
   lds_barrier();  // A_II visible; the off-diagonal operands are dead
 
   // xw, column-major (channel rows, token columns), by identity transposes
 #pragma unroll
-  for (int ct = 0; ct < KT; ++ct) {
+  for (int ct = 0; ct < KTL; ++ct) {
     const f32x4 tr = mfma_f16(xw8[ct >> 1], sel_h[ct & 1], zero4());
     f16x4 o4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o4[e] = (_Float16)tr[e];
-    *(f16x4*)(&xw_s[(16 * ct + lr) * XP + 16 * wave + 4 * lg]) = o4;
+    *(f16x4*)(&xw_s[(16 * (2 * sg0 + ct) + lr) * XP + 16 * wave + 4 * lg]) = o4;
   }
 
   // ---- A_IJ = -A_II sum_{M=J}^{I-1} L_IM A_MJ, stage d = I - J ----
 #pragma unroll
   for (int d = 1; d <= 3; ++d) {
-    if (wave >= d) {
+    if (cg == 0 && wave >= d) {
       const int J = wave - d;
       f32x4 T = zero4();
 #pragma unroll
@@ -613,7 +667,8 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     const bool two = R >= 2;  // row blocks 0, 1 have no entries past token 31
     _Float16* W_out = a.out.W + unit * (size_t)(C * K);
 #pragma unroll
-    for (int ct = 0; ct < KT; ++ct) {
+    for (int ctl = 0; ctl < KTL; ++ctl) {
+      const int ct = 2 * sg0 + ctl;  // this group's channel tiles
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -631,7 +686,8 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     }
     _Float16* U_out = a.out.U + unit * (size_t)(C * V);
 #pragma unroll
-    for (int ct = 0; ct < VT; ++ct) {
+    for (int ctl = 0; ctl < VTL; ++ctl) {
+      const int ct = 2 * vg0 + ctl;  // this group's value tiles
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -649,7 +705,7 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
     }
   }
   if (a.A_ref != nullptr) {
-    for (int idx = tid; idx < len * C; idx += 256) {
+    for (int idx = tid; idx < len * C; idx += NT) {
       const int tt = idx / C, j = idx % C;
       a.A_ref[((size_t)(tok0 + tt) * H + h) * C + j] = (__bf16)As_s[tt * AP + j];
     }
@@ -658,14 +714,14 @@ __global__ __launch_bounds__(256, K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
 
 template <int K, int V, bool CAUSAL>
 hipError_t launch_raw(const WyArgs& a, int n_chunk, hipStream_t stream) {
-  hipLaunchKernelGGL((wy_kernel<K, V, CAUSAL, false, false, __bf16, true>), dim3(n_chunk, a.H), dim3(256), 0,
-                     stream, a);
+  hipLaunchKernelGGL((wy_kernel<K, V, CAUSAL, false, false, __bf16, true>), dim3(n_chunk, a.H),
+                     dim3(256 * wy_groups(K)), 0, stream, a);
   return hipGetLastError();
 }
 
 template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM>
 hipError_t launch_t(const WyArgs& a, int n_chunk, bool beta_bf16, hipStream_t stream) {
-  dim3 grid(n_chunk, a.H), block(256);
+  dim3 grid(n_chunk, a.H), block(256 * wy_groups(K));
   if (beta_bf16)
     hipLaunchKernelGGL((wy_kernel<K, V, CAUSAL, HAS_B, G_CUM, __bf16>), grid, block, 0, stream, a);
   else
