@@ -156,7 +156,8 @@ size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int 
  *   read_states [n_block, H, K, V] fp32, used by out_mode = SNAPSHOT
  *   snaps    [n_block, H, K, V] fp32 state before each block-start chunk, or NULL
  *   o        [T, H, V] bf16 output (out_mode != NONE)
- * K, V in {64, 128, 256}.  The workspace must hold
+ * K, V in {64, 128, 256, 512} with K == V; at 512 only MEMT_GDN2_OUT_NONE and
+ * MEMT_GDN2_OUT_SNAPSHOT (no causal output).  The workspace must hold
  * memt_gdn2_chunk_update_workspace_size(...) bytes, 256-byte aligned.
  */
 int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g,
@@ -277,7 +278,7 @@ int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void*
  *   beta   [T,H,D] bf16 = sigmoid(write)
  * decay, erase, write: bf16 rows of H*D channels, `*_stride` elements apart
  * (views of the projection outputs; stride >= H*D, a multiple of 8);
- * decay_bias [H*D] bf16, decay_scale_log [H] bf16.  D in {64, 128, 256}.
+ * decay_bias [H*D] bf16, decay_scale_log [H] bf16.  D in {64, 128, 256, 512}.
  * Inputs and outputs 16-byte aligned.
  */
 int memt_gdn2_write_gates(const void* decay, int64_t decay_stride, const void* decay_bias,

@@ -7,7 +7,10 @@ using namespace memt;
 
 namespace {
 
-bool supported_kv(int K, int V) { return K == V && (K == 64 || K == 128 || K == 256); }
+bool supported_kv(int K, int V) { return K == V && (K == 64 || K == 128 || K == 256 || K == 512); }
+// d = 512 has no causal output and no raw-projection path (its model reads
+// memory through the snapshot read only)
+bool wide_ok(int K, bool causal, bool raw) { return K <= 256 || (!causal && !raw); }
 
 int status_of(hipError_t e) { return e == hipSuccess ? MEMT_GDN2_OK : MEMT_GDN2_ELAUNCH; }
 
@@ -28,7 +31,7 @@ int prologue_common(PrologueArgs& a, const void* decay, int64_t decay_stride, co
                     const void* decay_scale_log, const void* erase, int64_t erase_stride, const void* write,
                     int64_t write_stride, float* g, void* beta, int64_t T, int H, int D) {
   if (T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
-  if (D != 64 && D != 128 && D != 256) return MEMT_GDN2_EUNSUPPORTED;
+  if (D != 64 && D != 128 && D != 256 && D != 512) return MEMT_GDN2_EUNSUPPORTED;
   const int64_t width = (int64_t)H * D;
   if (T > 0) {
     if (!row_operand_ok(decay, decay_stride, width) || !row_operand_ok(erase, erase_stride, width) ||
@@ -136,6 +139,7 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
   if (out_mode != MEMT_GDN2_OUT_NONE && out_mode != MEMT_GDN2_OUT_SNAPSHOT && out_mode != MEMT_GDN2_OUT_CAUSAL)
     return MEMT_GDN2_EINVAL;
+  if (!wide_ok(K, out_mode == MEMT_GDN2_OUT_CAUSAL, x != nullptr)) return MEMT_GDN2_EUNSUPPORTED;
   if (plan->n_chunk > 0) {
     if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || plan->seq_chunk_offsets == nullptr)
       return MEMT_GDN2_EINVAL;
@@ -273,6 +277,7 @@ int memt_gdn2_wy_fwd(const void* q, const void* k, const void* v, const float* g
   if (plan->n_chunk > 0 && (k == nullptr || v == nullptr || gk == nullptr || beta == nullptr)) return MEMT_GDN2_EINVAL;
   if ((Aqk != nullptr || qg != nullptr) && q == nullptr) return MEMT_GDN2_EINVAL;
   const bool causal = q != nullptr;
+  if (!wide_ok(K, causal, false)) return MEMT_GDN2_EUNSUPPORTED;
   const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, causal);
   if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
     return MEMT_GDN2_EWORKSPACE;
@@ -338,7 +343,7 @@ int memt_gdn2_fwd_h(const void* kg, const void* w, const void* u, const float* g
 int memt_gdn2_read_fwd(const void* q, const float* snaps, void* o, const memt_gdn2_plan* plan, int64_t T, int H,
                        int K, int V, float scale, void* stream) {
   if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
-  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
   if (plan->n_chunk > 0 && (q == nullptr || snaps == nullptr || o == nullptr || plan->chunk_block_ids == nullptr))
     return MEMT_GDN2_EINVAL;
   if (!aligned16(q) || !aligned16(snaps)) return MEMT_GDN2_EINVAL;
@@ -350,7 +355,7 @@ int memt_gdn2_read_fwd_slots(const void* q, const float* pool, int n_slots, cons
                              const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale, void* stream) {
   if (pool == nullptr || n_slots <= 0 || read_slot == nullptr) return MEMT_GDN2_EINVAL;
   if (!plan_ok(plan) || T < 0 || H <= 0) return MEMT_GDN2_EINVAL;
-  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
   if (plan->n_chunk > 0 && (q == nullptr || o == nullptr || plan->chunk_block_ids == nullptr)) return MEMT_GDN2_EINVAL;
   if (!aligned16(q) || !aligned16(pool)) return MEMT_GDN2_EINVAL;
   return status_of(launch_read_fwd((const __bf16*)q, pool, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
@@ -373,7 +378,7 @@ int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void*
                             const void* weight, void* out, int B, int H, int K, int V, float scale, float eps,
                             float softcap, int gate_kind, void* stream) {
   if (B < 0 || H <= 0) return MEMT_GDN2_EINVAL;
-  if (!((K == 64 && V == 64) || (K == 128 && V == 128) || (K == 256 && V == 256))) return MEMT_GDN2_EUNSUPPORTED;
+  if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
   if (B > 0 && (S == nullptr || q == nullptr || gate == nullptr || weight == nullptr || out == nullptr))
     return MEMT_GDN2_EINVAL;
   if (!aligned16(S)) return MEMT_GDN2_EINVAL;

@@ -134,17 +134,20 @@ struct GroupBuffers {
 };
 
 // State columns one scan workgroup carries: all of them up to d = 128; at
-// d = 256 a 64-column slice, so that the K x 64 fp32 slice and the prefetched
-// chunk records fit the registers of two waves per SIMD.
-__host__ __device__ constexpr int scan_slice(int D) { return D > 128 ? 64 : D; }
+// d = 256 a 64-column slice and at d = 512 a 32-column slice, so that the
+// K x slice fp32 state and the prefetched chunk records fit the registers of
+// two waves per SIMD.
+__host__ __device__ constexpr int scan_slice(int D) { return D > 256 ? 32 : D > 128 ? 64 : D; }
 
 // Chunks per group for the two-level scan (0 = plain per-sequence scan).
 // The scan runs one workgroup per (sequence or group, head, column slice).
 // Groups are used when the plain scan would occupy fewer than 256 workgroups
 // (one per CU of the MI355X) and the sequences are long; L is the smallest
 // power of two >= 4 that keeps the per-group grid within 256 workgroups.
+// d = 512 always runs the plain scan: its group transition (K x K fp32 per
+// head) does not fit the transition and combine kernels' register plans.
 inline int scan_group_chunks(int n_chunk, int n_seq, int H, int V) {
-  if (n_seq <= 0 || n_chunk <= 0) return 0;
+  if (n_seq <= 0 || n_chunk <= 0 || V > 256) return 0;
   const long hs = (long)H * (V / scan_slice(V));
   if ((long)n_seq * hs >= 256) return 0;
   int L = 4;

@@ -7,54 +7,68 @@ namespace {
 // ---------------------------------------------------------------------------
 // Snapshot reader (models/qwen/ops/_triton/read.py:22-71): per (chunk, head),
 // o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32 accumulation.
-// Wave w handles token rows [16w, 16w + 16) and all V columns.
+// A workgroup takes CB state columns (all of them up to d = 256) of one head
+// for a run of `per` consecutive chunks, and reloads the bf16 state tile only
+// when the block changes.  Wave w handles token rows [16w, 16w + 16).
 // ---------------------------------------------------------------------------
+__host__ __device__ constexpr int read_cols(int V) { return V > 256 ? 64 : V; }
+constexpr int kReadChunksPerGroup = 4;  // chunks per reader workgroup
+
 template <int K, int V>
 __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict__ q,
                                                        const float* __restrict__ snaps,
                                                        __bf16* __restrict__ o, const int32_t* chunk_tok0,
                                                        const int32_t* chunk_len, const int32_t* block_ids,
-                                                       int H, float scale, const int32_t* block_slot) {
-  constexpr int SKP = K + 8;
-  __shared__ __attribute__((aligned(16))) __bf16 S_lds[V * SKP];  // column-major bf16(S)
-  const int chunk = blockIdx.x, h = blockIdx.y;
+                                                       int n_chunk, int per, int H, float scale,
+                                                       const int32_t* block_slot) {
+  constexpr int CB = read_cols(V), SKP = K + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 S_lds[CB * SKP];  // column-major bf16(S), CB columns
+  const int h = blockIdx.y, col0 = blockIdx.z * CB;
+  const int c_begin = blockIdx.x * per, c_end = min(c_begin + per, n_chunk);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
-  const int blk = block_ids[chunk];
-  const float* Sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V;
-  for (int idx = tid; idx < K * V / 4; idx += 256) {
-    const int row = idx / (V / 4), c4 = (idx % (V / 4)) * 4;
-    const f32x4 s4 = *(const f32x4*)(Sp + (size_t)row * V + c4);
+  int loaded = -1;
+  for (int chunk = c_begin; chunk < c_end; ++chunk) {
+    const int tok0 = chunk_tok0[chunk], len = chunk_len[chunk];
+    const int blk = block_ids[chunk];
+    if (blk != loaded) {
+      if (loaded >= 0) __syncthreads();  // every wave is done with the previous tile
+      const float* Sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V + col0;
+      for (int idx = tid; idx < K * CB / 4; idx += 256) {
+        const int row = idx / (CB / 4), c4 = (idx % (CB / 4)) * 4;
+        const f32x4 s4 = *(const f32x4*)(Sp + (size_t)row * V + c4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) S_lds[(c4 + e) * SKP + row] = (__bf16)s4[e];
+        for (int e = 0; e < 4; ++e) S_lds[(c4 + e) * SKP + row] = (__bf16)s4[e];
+      }
+      __syncthreads();
+      loaded = blk;
+    }
+    const int t = 16 * w + lr;
+    f32x4 acc[CB / 16];
+#pragma unroll
+    for (int ct = 0; ct < CB / 16; ++ct) acc[ct] = zero4();
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+      bf16x8 qa;
+      if (t < len) {
+        qa = *(const bf16x8*)(q + ((size_t)(tok0 + t) * H + h) * K + 32 * s + 8 * lg);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qa[e] = (__bf16)0.f;
+      }
+#pragma unroll
+      for (int ct = 0; ct < CB / 16; ++ct) {
+        const bf16x8 sb = *(const bf16x8*)(&S_lds[(16 * ct + lr) * SKP + 32 * s + 8 * lg]);
+        acc[ct] = mfma_bf16(qa, sb, acc[ct]);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CB / 16; ++ct)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tt = 16 * w + 4 * lg + e;
+        if (tt < len) o[((size_t)(tok0 + tt) * H + h) * V + col0 + 16 * ct + lr] = (__bf16)(acc[ct][e] * scale);
+      }
   }
-  __syncthreads();
-  const int t = 16 * w + lr;
-  f32x4 acc[V / 16];
-#pragma unroll
-  for (int ct = 0; ct < V / 16; ++ct) acc[ct] = zero4();
-#pragma unroll
-  for (int s = 0; s < K / 32; ++s) {
-    bf16x8 qa;
-    if (t < len) {
-      qa = *(const bf16x8*)(q + ((size_t)(tok0 + t) * H + h) * K + 32 * s + 8 * lg);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qa[e] = (__bf16)0.f;
-    }
-#pragma unroll
-    for (int ct = 0; ct < V / 16; ++ct) {
-      const bf16x8 sb = *(const bf16x8*)(&S_lds[(16 * ct + lr) * SKP + 32 * s + 8 * lg]);
-      acc[ct] = mfma_bf16(qa, sb, acc[ct]);
-    }
-  }
-#pragma unroll
-  for (int ct = 0; ct < V / 16; ++ct)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int tt = 16 * w + 4 * lg + e;
-      if (tt < len) o[((size_t)(tok0 + tt) * H + h) * V + 16 * ct + lr] = (__bf16)(acc[ct][e] * scale);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -85,21 +99,25 @@ __device__ __forceinline__ __bf16 norm_gate_one(float x, float rs, float wt, flo
 // barriers, so the state stream starts at once; with more than NB rows per
 // thread each consumed row is replaced by the next one (a rolling window).
 // ---------------------------------------------------------------------------
+// Threads of a readout workgroup: one per value column at d = 512.
+__host__ __device__ constexpr int readout_threads(int V) { return V > 256 ? V : 256; }
+
 template <int K, int V>
-__global__ __launch_bounds__(256) void readout_kernel(const float* __restrict__ S, const int32_t* slot_idx,
+__global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float* __restrict__ S, const int32_t* slot_idx,
                                                       const __bf16* __restrict__ q,
                                                       const __bf16* __restrict__ gate,
                                                       const __bf16* __restrict__ weight,
                                                       __bf16* __restrict__ out, int H, float scale,
                                                       float eps, float softcap, int gate_kind) {
+  constexpr int NT = readout_threads(V);
   constexpr int CG = V / 4;          // float4 column groups
-  constexpr int RG = 256 / CG;       // row groups
+  constexpr int RG = NT / CG;        // row groups
   constexpr int RPT = K / RG;        // rows per thread
   constexpr int NB = RPT < 16 ? RPT : 16;  // state rows in flight per thread
-  static_assert(RG * CG == 256 && RPT * RG == K && RPT % NB == 0, "readout tiling");
-  __shared__ float q_s[K > 256 ? K : 256];  // every thread stores: no branch before the first wait
+  static_assert(RG * CG == NT && RPT * RG == K && RPT % NB == 0 && K <= NT, "readout tiling");
+  __shared__ float q_s[NT];  // every thread stores: no branch before the first wait
   __shared__ float part[RG][V];
-  __shared__ float red[4];
+  __shared__ float red[NT / 64];
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int tid = threadIdx.x;
   const int slot = slot_idx ? slot_idx[b] : b;
@@ -297,35 +315,38 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
                            int K, int V, float scale, hipStream_t stream, const int32_t* block_slot) {
   if (n_chunk == 0) return hipSuccess;
-  dim3 grid(n_chunk, H), block(256);
-  if (K == 64 && V == 64)
-    hipLaunchKernelGGL((read_fwd_kernel<64, 64>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale, block_slot);
-  else if (K == 128 && V == 128)
-    hipLaunchKernelGGL((read_fwd_kernel<128, 128>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale, block_slot);
-  else if (K == 256 && V == 256)
-    hipLaunchKernelGGL((read_fwd_kernel<256, 256>), grid, block, 0, stream, q, snaps, o, chunk_tok0, chunk_len,
-                       chunk_block_ids, H, scale, block_slot);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  // chunks per workgroup: the tile of a block is read once per run of chunks
+  const int per = kReadChunksPerGroup;
+  const unsigned runs = (unsigned)((n_chunk + per - 1) / per);
+#define MEMT_RD(KK, VV)                                                                                      \
+  if (K == KK && V == VV) {                                                                                  \
+    hipLaunchKernelGGL((read_fwd_kernel<KK, VV>), dim3(runs, H, VV / read_cols(VV)), dim3(256), 0, stream, q, \
+                       snaps, o, chunk_tok0, chunk_len, chunk_block_ids, n_chunk, per, H, scale, block_slot);  \
+    return hipGetLastError();                                                                                \
+  }
+  MEMT_RD(64, 64)
+  MEMT_RD(128, 128)
+  MEMT_RD(256, 256)
+  MEMT_RD(512, 512)
+#undef MEMT_RD
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
                           const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
                           float eps, float softcap, int gate_kind, hipStream_t stream) {
   if (B == 0) return hipSuccess;
-  dim3 grid(B * H), block(256);
+  dim3 grid(B * H);
 #define MEMT_RO(KK, VV)                                                                                   \
   if (K == KK && V == VV) {                                                                               \
-    hipLaunchKernelGGL((readout_kernel<KK, VV>), grid, block, 0, stream, S, slot_idx, q, gate, weight, out, \
-                       H, scale, eps, softcap, gate_kind);                                                \
+    hipLaunchKernelGGL((readout_kernel<KK, VV>), grid, dim3(readout_threads(VV)), 0, stream, S, slot_idx, q, \
+                       gate, weight, out, H, scale, eps, softcap, gate_kind);                             \
     return hipGetLastError();                                                                             \
   }
   MEMT_RO(64, 64)
   MEMT_RO(128, 128)
   MEMT_RO(256, 256)
+  MEMT_RO(512, 512)
 #undef MEMT_RO
   return hipErrorInvalidValue;
 }
@@ -383,6 +404,9 @@ hipError_t launch_wy_export(const WyBuffers& in, const int32_t* chunk_tok0, cons
   else if (K == 256 && V == 256)
     hipLaunchKernelGGL((wy_export_kernel<256, 256>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
                        Aqk, qg);
+  else if (K == 512 && V == 512)
+    hipLaunchKernelGGL((wy_export_kernel<512, 512>), grid, block, 0, stream, in, chunk_tok0, chunk_len, H, w, u, kg,
+                       Aqk, qg);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -401,6 +425,9 @@ hipError_t launch_wy_import(const __bf16* w, const __bf16* u, const __bf16* kg, 
                        out);
   else if (K == 256 && V == 256)
     hipLaunchKernelGGL((wy_import_kernel<256, 256>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
+                       out);
+  else if (K == 512 && V == 512)
+    hipLaunchKernelGGL((wy_import_kernel<512, 512>), grid, block, 0, stream, w, u, kg, gk, chunk_tok0, chunk_len, H,
                        out);
   else
     return hipErrorInvalidValue;

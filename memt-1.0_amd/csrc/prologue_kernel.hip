@@ -138,6 +138,8 @@ hipError_t launch_prologue(const PrologueArgs& a, int D, bool qk, hipStream_t st
       return launch_d<128>(a, qk, stream);
     case 256:
       return launch_d<256>(a, qk, stream);
+    case 512:
+      return launch_d<512>(a, qk, stream);
     default:
       return hipErrorInvalidValue;
   }

@@ -608,19 +608,28 @@ __global__ __launch_bounds__(256) void combine_kernel(StateArgs a) {
 
 template <int K, int V>
 hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
-  int units = a.n_seq;
-  if (a.group_L > 0) {
-    units = group_bound(a.n_chunk, a.n_seq, a.group_L);
-    const int nt = units * a.H * (K / scan_slice(K) + V / scan_slice(V));
-    hipLaunchKernelGGL((trans_kernel<K, V>), dim3(nt), dim3(kScanThreads), 0, stream, a, units);
-    hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 16) * a.H * a.n_seq), dim3(256), 0, stream, a);
+  if constexpr (K > 256) {
+    // d = 512: the plain scan without the causal output (the final-state and
+    // snapshot-read modes of the wide-state model)
+    if (causal || a.group_L > 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((state_kernel<K, V, false>), dim3(a.n_seq * a.H * (V / scan_slice(V))), dim3(kScanThreads),
+                       0, stream, a, a.n_seq);
+    return hipGetLastError();
+  } else {
+    int units = a.n_seq;
+    if (a.group_L > 0) {
+      units = group_bound(a.n_chunk, a.n_seq, a.group_L);
+      const int nt = units * a.H * (K / scan_slice(K) + V / scan_slice(V));
+      hipLaunchKernelGGL((trans_kernel<K, V>), dim3(nt), dim3(kScanThreads), 0, stream, a, units);
+      hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 16) * a.H * a.n_seq), dim3(256), 0, stream, a);
+    }
+    const dim3 grid(units * a.H * (V / scan_slice(V))), block(kScanThreads);
+    if (causal)
+      hipLaunchKernelGGL((state_kernel<K, V, true>), grid, block, 0, stream, a, units);
+    else
+      hipLaunchKernelGGL((state_kernel<K, V, false>), grid, block, 0, stream, a, units);
+    return hipGetLastError();
   }
-  const dim3 grid(units * a.H * (V / scan_slice(V))), block(kScanThreads);
-  if (causal)
-    hipLaunchKernelGGL((state_kernel<K, V, true>), grid, block, 0, stream, a, units);
-  else
-    hipLaunchKernelGGL((state_kernel<K, V, false>), grid, block, 0, stream, a, units);
-  return hipGetLastError();
 }
 
 }  // namespace
@@ -630,6 +639,7 @@ hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream
   if (K == 64 && V == 64) return launch_t<64, 64>(a, causal, stream);
   if (K == 128 && V == 128) return launch_t<128, 128>(a, causal, stream);
   if (K == 256 && V == 256) return launch_t<256, 256>(a, causal, stream);
+  if (K == 512 && V == 512) return launch_t<512, 512>(a, causal, stream);
   return hipErrorInvalidValue;
 }
 

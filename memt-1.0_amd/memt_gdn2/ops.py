@@ -155,6 +155,8 @@ def chunk_gdn2_fwd_intra(q, k, v, gk, b, w_gate, scale, cu_seqlens=None, chunk_s
     Returns ``(w, u, qg, kg, Aqk, Akk)`` in the reference layouts (bf16
     [B,T,H,*]); ``qg`` is None unless ``disable_recompute``.  ``gk`` is the
     chunk-local cumulative decay in log2 units; ``b`` may be None (unit erase).
+    ``q`` may be None (the Flash write-only intra,
+    models/deepseek/ops/_triton/intra.py:391-448): ``Aqk`` then stays zero.
     """
     lib = _lib.load()
     _lib.require_gpu(q, k, v, gk, b, w_gate)
@@ -174,14 +176,17 @@ def chunk_gdn2_fwd_intra(q, k, v, gk, b, w_gate, scale, cu_seqlens=None, chunk_s
     kg = torch.empty_like(k)
     Aqk = torch.zeros(B, T, H, chunk_size, dtype=k.dtype, device=dev)
     Akk = torch.zeros(B, T, H, chunk_size, dtype=k.dtype, device=dev)
+    if q is None and disable_recompute:
+        raise ValueError("disable_recompute needs q (qg = q * 2^gk)")
     qg = torch.empty_like(q) if disable_recompute else None
-    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "causal"))
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, K, V, "causal" if q is not None else "none"))
     p = plan.abi()
     _lib.check(
         lib.memt_gdn2_wy_fwd(
             _lib.ptr(q), k.data_ptr(), v.data_ptr(), gk.data_ptr(), _lib.ptr(b), w_gate.data_ptr(), _DT[w_gate.dtype],
             ctypes.byref(p), B * T, H, K, V, float(scale), w.data_ptr(), u.data_ptr(), kg.data_ptr(),
-            Akk.data_ptr(), Aqk.data_ptr(), _lib.ptr(qg), ws.data_ptr(), ws.numel(), _lib.stream_of(dev)),
+            Akk.data_ptr(), Aqk.data_ptr() if q is not None else None, _lib.ptr(qg), ws.data_ptr(), ws.numel(),
+            _lib.stream_of(dev)),
         "chunk_gdn2_fwd_intra",
     )
     return w, u, qg, kg, Aqk, Akk

@@ -52,7 +52,7 @@ def _ref_gates(decay, bias, rate, erase, write, H):
     return g, sb, beta
 
 
-@pytest.mark.parametrize("T,H,D", [(37, 4, 128), (64, 2, 64), (9, 2, 256), (1, 16, 128)])
+@pytest.mark.parametrize("T,H,D", [(37, 4, 128), (64, 2, 64), (9, 2, 256), (1, 16, 128), (11, 2, 512)])
 def test_write_gates(dev, T, H, D):
     print(f"write_gates T={T} H={H} D={D}", flush=True)
     _, _, decay, bias, rate, erase, write = _fused_rows(T, H, D, dev, seed=T + D)
@@ -64,7 +64,7 @@ def test_write_gates(dev, T, H, D):
     _bf16_close(host(beta).reshape(T, -1), beta_ref)
 
 
-@pytest.mark.parametrize("T,H,D", [(100, 4, 128), (33, 2, 64), (17, 2, 256)])
+@pytest.mark.parametrize("T,H,D", [(100, 4, 128), (33, 2, 64), (17, 2, 256), (13, 2, 512)])
 def test_memory_prologue(dev, T, H, D):
     print(f"memory_prologue T={T} H={H} D={D}", flush=True)
     q, k, decay, bias, rate, erase, write = _fused_rows(T, H, D, dev, seed=7 * T + D)
