@@ -243,6 +243,28 @@ def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32):
     }
 
 
+def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8):
+    """The Flash model's memory shape (d=512, models/deepseek/ops/packed.py:70-108):
+    a commit in snapshot mode (every token reads the incoming state, final
+    state out) and a batch-B decode readout."""
+    steps = min(steps, 10)
+    up = bench_update(dev, steps, warmup, T, H, D, out_mode="snapshot", on_device=True)
+    ro = bench_readout(dev, steps, warmup, B=B, H=H, D=D)
+    ub, uf = update_bytes(T, H, D, D), update_flops(T, H, D, D, causal=False) + 2 * T * H * D * D
+    t = up["event_ms_mean"] * 1e-3
+    return {
+        "metric": "Flash-shape GDN-2 commit tokens/s @H64 d512 T8K; decode readout GB/s @B8",
+        "value": T / (up["ms_per_step"] * 1e-3), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": up["ms_per_step"], "dtype": "bf16", "data": "synthetic (same distributions, drawn on the GPU)",
+        "config": {"workload": f"chunked GDN-2 commit, B=1 H={H} T={T} dk=dv={D} chunk=64, snapshot read + final state"},
+        "roofline": {"bound": "hbm", "achieved": ub / t / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ub / t / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": ub,
+                     "mfma_frac": uf / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, "algorithmic_flops": uf},
+        "readout": {"workload": f"decode readout B={B} H={H} dk=dv={D}", "value": ro["gbs"], "unit": "GB/s",
+                    "us_per_launch": ro["ms_per_launch"] * 1e3, "frac": ro["gbs"] / HBM_PEAK_GBS},
+    }
+
+
 def calibrate(dev, T=8192, H=16, D=128, reps=3):
     """Workload for hardware-counter runs (rocprofv3 --pmc): a device copy of
     COPY_BYTES (the reference for FETCH_SIZE / WRITE_SIZE per byte), then `reps`
@@ -326,6 +348,8 @@ def main():
     ap.add_argument("--mode", default="causal", choices=["causal", "snapshot"])
     ap.add_argument("--wide", action="store_true",
                     help="measure the wide-state workload instead (B=1 H=64 T=16384 d=256; batch-32 readout)")
+    ap.add_argument("--flash", action="store_true",
+                    help="measure the Flash memory shape instead (B=1 H=64 T=8192 d=512 commit; batch-8 readout)")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the hardware-counter workload (copy of known size, then update steps and readouts)")
     args = ap.parse_args()
@@ -347,6 +371,9 @@ def main():
         return
     if args.wide:
         print(json.dumps(bench_wide(dev, args.steps, args.warmup)))
+        return
+    if args.flash:
+        print(json.dumps(bench_flash(dev, args.steps, args.warmup)))
         return
 
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)

@@ -10,21 +10,30 @@ namespace {
 // A workgroup takes CB state columns (all of them up to d = 256) of one head
 // for a run of `per` consecutive chunks, and reloads the bf16 state tile only
 // when the block changes.  Wave w handles token rows [16w, 16w + 16).
+// With several column tiles (d = 512), the NCB workgroups of one (run, head)
+// read the same q rows: their block indices are 8 apart, so they share an XCD
+// (blocks go to the eight XCDs round-robin) and run together, and q comes from
+// that XCD's L2 after its first read.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int read_cols(int V) { return V > 256 ? 64 : V; }
-constexpr int kReadChunksPerGroup = 4;  // chunks per reader workgroup
+// chunks per reader workgroup: a run shares one state tile load
+__host__ __device__ constexpr int read_run(int V) { return V > 256 ? 16 : 4; }
 
 template <int K, int V>
 __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict__ q,
                                                        const float* __restrict__ snaps,
                                                        __bf16* __restrict__ o, const int32_t* chunk_tok0,
                                                        const int32_t* chunk_len, const int32_t* block_ids,
-                                                       int n_chunk, int per, int H, float scale,
+                                                       int n_chunk, int n_units, int H, float scale,
                                                        const int32_t* block_slot) {
-  constexpr int CB = read_cols(V), SKP = K + 8;
+  constexpr int CB = read_cols(V), NCB = V / CB, SKP = K + 8, per = read_run(V);
   __shared__ __attribute__((aligned(16))) __bf16 S_lds[CB * SKP];  // column-major bf16(S), CB columns
-  const int h = blockIdx.y, col0 = blockIdx.z * CB;
-  const int c_begin = blockIdx.x * per, c_end = min(c_begin + per, n_chunk);
+  // block b -> column tile (b / 8) % NCB of unit (b % 8) + 8 (b / (8 NCB)); a unit is (run, head)
+  const int b = blockIdx.x;
+  const int unit = NCB == 1 ? b : (b & 7) + 8 * (b / (8 * NCB));
+  if (unit >= n_units) return;
+  const int h = unit % H, col0 = (NCB == 1 ? 0 : (b >> 3) % NCB) * CB;
+  const int c_begin = (unit / H) * per, c_end = min(c_begin + per, n_chunk);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   int loaded = -1;
   for (int chunk = c_begin; chunk < c_end; ++chunk) {
@@ -315,14 +324,14 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
                            int K, int V, float scale, hipStream_t stream, const int32_t* block_slot) {
   if (n_chunk == 0) return hipSuccess;
-  // chunks per workgroup: the tile of a block is read once per run of chunks
-  const int per = kReadChunksPerGroup;
-  const unsigned runs = (unsigned)((n_chunk + per - 1) / per);
-#define MEMT_RD(KK, VV)                                                                                      \
-  if (K == KK && V == VV) {                                                                                  \
-    hipLaunchKernelGGL((read_fwd_kernel<KK, VV>), dim3(runs, H, VV / read_cols(VV)), dim3(256), 0, stream, q, \
-                       snaps, o, chunk_tok0, chunk_len, chunk_block_ids, n_chunk, per, H, scale, block_slot);  \
-    return hipGetLastError();                                                                                \
+  const int runs = (n_chunk + read_run(V) - 1) / read_run(V), n_units = runs * H;
+  // units rounded up to a multiple of 8 when a unit has several column tiles
+  const int ncb = V / read_cols(V), n_blocks = ncb == 1 ? n_units : (n_units + 7) / 8 * 8 * ncb;
+#define MEMT_RD(KK, VV)                                                                                        \
+  if (K == KK && V == VV) {                                                                                    \
+    hipLaunchKernelGGL((read_fwd_kernel<KK, VV>), dim3(n_blocks), dim3(256), 0, stream, q, snaps, o, chunk_tok0, \
+                       chunk_len, chunk_block_ids, n_chunk, n_units, H, scale, block_slot);                    \
+    return hipGetLastError();                                                                                  \
   }
   MEMT_RD(64, 64)
   MEMT_RD(128, 128)
