@@ -445,18 +445,30 @@ __global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a, int un
   scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds);
 }
 
-// Phase 1 of the two-level scan: the first (K / slice) units H blocks form
-// P_g, the rest Q_g.
+// Phase 1 of the two-level scan: nP = (K / slice) units H blocks form P_g and
+// as many form Q_g.  The P and Q blocks of one (group, head, slice) read the
+// same W and kg^T records, so they are interleaved in runs of 8 (blocks b and
+// b + 8 of every 16): the pair shares an XCD and its L2 and runs at the same
+// time.
 template <int K, int V>
 __global__ __launch_bounds__(kScanThreads) void trans_kernel(StateArgs a, int units) {
   constexpr int NSK = scan_slice(K), NSV = scan_slice(V);
   constexpr int NCM = NSK > NSV ? NSK : NSV;
+  static_assert(K / NSK == V / NSV, "as many P as Q blocks");
   __shared__ __attribute__((aligned(16))) _Float16 S_lds[NCM * (K + kSPad)];
   __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NCM * (kChunk + kVPad)];
   const int per = units * a.H, nP = per * (K / NSK);
-  const int b = blockIdx.x < nP ? blockIdx.x : blockIdx.x - nP;
+  bool is_p;
+  int b;
+  if (nP % 8 == 0) {
+    is_p = ((blockIdx.x >> 3) & 1) == 0;
+    b = (blockIdx.x >> 4) * 8 + (blockIdx.x & 7);
+  } else {
+    is_p = (int)blockIdx.x < nP;
+    b = is_p ? blockIdx.x : blockIdx.x - nP;
+  }
   const int r = b % per, slice = b / per;
-  if (blockIdx.x < nP)
+  if (is_p)
     scan_body<K, V, NSK, false, 1>(a, r / a.H, r % a.H, NSK * slice, S_lds, Vn_lds);
   else
     scan_body<K, V, NSV, false, 2>(a, r / a.H, r % a.H, NSV * slice, S_lds, Vn_lds);
