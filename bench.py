@@ -342,8 +342,8 @@ def cpu_baseline_readout(B=64, H=16, D=128, runs=5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--mode", default="causal", choices=["causal", "snapshot"])
     ap.add_argument("--wide", action="store_true",
@@ -377,7 +377,8 @@ def main():
         return
 
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)
-    snap = bench_update(dev, max(10, args.steps // 2), 2, T, H, D, out_mode="snapshot") if args.mode == "causal" else None
+    snap = (bench_update(dev, max(10, args.steps // 2), args.warmup, T, H, D, out_mode="snapshot")
+            if args.mode == "causal" else None)
     ro = bench_readout(dev, args.steps, args.warmup)
     pro = bench_prologue(dev)
 

@@ -1,4 +1,4 @@
-// WY stage of the chunked GDN-2 update, one workgroup (4 waves) per (chunk, head).
+// WY stage of the chunked GDN-2 update, one workgroup per (chunk, head).
 //
 // For a chunk of C <= 64 tokens (rows past the chunk end are zero padded):
 //   gk    = 1/ln2 * cumsum_chunk(g)                       (FLA/ops/utils/cumsum.py:116-133)
@@ -36,7 +36,8 @@
 // Precision: every MFMA operand of the state scan (W, b k 2^gk, qg, beta v, A, U,
 // kg, Aqk) is fp16 with fp32 accumulation; gk, L, A are fp32.
 // LDS stays under 80 KB at d = 128, so two workgroups share a CU; d = 256 takes
-// 130 KB and one workgroup per CU.
+// 130 KB and one workgroup per CU.  From d = 128 on the workgroup has two
+// channel groups of 4 waves (8 waves); d = 512 runs two channel passes.
 #include <type_traits>
 
 #include "gdn2_internal.h"
@@ -53,9 +54,14 @@ __device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
 }
 
 // Channel groups of 4 waves: the K channels (and V value columns) split into
-// NCG groups, each handled by its own 4 waves with the d = 128 register plan;
-// the L / Aqk tiles are summed over the groups through LDS.
-__host__ __device__ constexpr int wy_groups(int K) { return K >= 256 ? 2 : 1; }
+// NCG groups, each handled by its own 4 waves; the L / Aqk tiles are summed
+// over the groups through LDS.  At d = 128 two groups of 64 channels halve the
+// registers per wave (at most 128: two 8-wave workgroups per CU, 16 waves to
+// hide the load latency, against 8 with one group); d = 256 keeps 128 channels
+// per group, one workgroup per CU (its LDS).
+__host__ __device__ constexpr int wy_groups(int K) { return K >= 128 ? 2 : 1; }
+// waves per SIMD the register budget is sized for
+__host__ __device__ constexpr int wy_waves_per_simd(int K) { return K == 128 ? 4 : K < 128 ? 2 : 1; }
 // Identity-matrix selectors: element j of lane (lr, lg) is 1 where the slot's channel
 // is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
 // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
@@ -77,7 +83,7 @@ __host__ __device__ constexpr int wy_passes(int K) { return K > 256 ? K / 256 : 
 // k_til = sqrt_b * l2norm(k) itself, in the prologue's op order, and writes
 // q_hat for the snapshot read.
 template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT, bool RAW = false>
-__global__ __launch_bounds__(256 * wy_groups(K), K <= 128 ? 2 : 1) void wy_kernel(WyArgs a) {
+__global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_kernel(WyArgs a) {
   static_assert(!RAW || (!HAS_B && !G_CUM), "raw projections carry the erase gate in k and g un-summed");
   constexpr int C = kChunk;
   constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;  // whole-head counts (record layouts)
