@@ -1,4 +1,4 @@
-"""Memory block of the Nano model on the HIP operators.
+"""Memory blocks of the Nano and Flash models on the HIP operators.
 
 ``QwenMemoryBlock`` keeps the reference block's parameter names and shapes
 (models/qwen/layer.py:34-69), so a checkpoint's state dict loads unchanged,
@@ -11,6 +11,11 @@ GEMMs (hipBLASLt).  Everything after them runs in this package's kernels:
   kernel (``fused_prologue=True``, the default), or one prologue kernel
   (gates, ``l2norm(q)``, ``sqrt_b * l2norm(k)``) then ``token_memory_packed``;
   then ``MemTRMSNormGated``.
+
+``DeepSeekMemoryBlock`` does the same for the Flash model
+(models/deepseek/layer.py:46-183): grouped low-rank Q/K/V and gate
+projections in torch, then the prologue kernel, ``token_memory_packed_flash``
+(or the snapshot read for queries) and the gated RMSNorm, at d = 512.
 """
 
 from __future__ import annotations
@@ -23,8 +28,9 @@ from torch.nn import functional as F
 
 from .layout import WY_TILE_TOKENS, build_chunk_plan, validate_packed_inputs
 from .norm import MemTRMSNormGated
-from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, token_memory_packed,
-                  token_memory_packed_fused, token_memory_packed_fused_slots, token_memory_packed_slots)
+from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, snapshot_read, token_memory_packed,
+                  token_memory_packed_flash, token_memory_packed_fused, token_memory_packed_fused_slots,
+                  token_memory_packed_slots)
 
 
 class QwenMemoryBlock(nn.Module):
@@ -141,5 +147,132 @@ class QwenMemoryBlock(nn.Module):
 
     def forward(self, hidden_states, initial_state, *, commit):
         """Single-request entry (models/qwen/layer.py:154-161)."""
+        return self.packed(hidden_states, initial_state, lengths=[len(hidden_states)], commit=commit,
+                           write_states=initial_state)
+
+
+def _latent_norm(inputs, weight, eps):
+    """RMS norm of a latent in fp32, back to the input dtype
+    (models/deepseek/ops/compiled_tensor_ops.py:12-20)."""
+    value = inputs.float() if inputs.dtype in (torch.bfloat16, torch.float16) else inputs
+    return (value * torch.rsqrt(value.square().mean(-1, keepdim=True) + eps) * weight.to(value.dtype)).to(inputs.dtype)
+
+
+class _LatentNorm(nn.Module):
+    def __init__(self, rank, eps):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(rank))
+        self.eps = eps
+
+
+class DeepSeekMemoryBlock(nn.Module):
+    """The Flash memory block, with the reference's parameter names and shapes
+    (models/deepseek/layer.py:54-107).  ``memory_config`` needs
+    ``hidden_size``, ``num_heads``, ``head_dim``, ``kv_groups``, ``q_rank``,
+    ``kv_rank``, ``gate_rank``, ``chunk_tokens``, ``norm_eps`` and
+    ``output_softcap``.  Every token reads the incoming state; a commit also
+    returns the final state."""
+
+    def __init__(self, memory_config, *, device=None):
+        super().__init__()
+        c = memory_config
+        self.hidden_size = c.hidden_size
+        self.num_heads = c.num_heads
+        self.head_dim = c.head_dim
+        self.value_dim = c.num_heads * c.head_dim
+        self.read_scale = c.head_dim ** -0.5
+        self.kv_groups = c.kv_groups
+        self.chunk_tokens = c.chunk_tokens
+        self.norm_eps = c.norm_eps
+        self.gate_rows = (c.gate_rank,) * 4
+        self.qkv_rows = (c.q_rank, c.kv_groups * c.kv_rank, c.kv_groups * c.kv_rank)
+        self.in_proj = nn.Linear(c.hidden_size, sum(self.qkv_rows) + sum(self.gate_rows), bias=False)
+        self.q_norm = _LatentNorm(c.q_rank, c.norm_eps)
+        self.q_up = nn.Linear(c.q_rank, self.value_dim, bias=False)
+        group_width = self.value_dim // c.kv_groups
+        self.k_group_up = nn.Parameter(torch.empty(c.kv_groups, group_width, c.kv_rank))
+        self.v_group_up = nn.Parameter(torch.empty(c.kv_groups, group_width, c.kv_rank))
+        self.k_group_norm = nn.Parameter(torch.ones(c.kv_groups, c.kv_rank))
+        self.v_group_norm = nn.Parameter(torch.ones(c.kv_groups, c.kv_rank))
+        self.b_up = nn.Linear(c.gate_rank, self.value_dim, bias=False)
+        self.w_up = nn.Linear(c.gate_rank, self.value_dim, bias=False)
+        self.f_down = nn.Linear(c.gate_rank, self.value_dim, bias=False)
+        self.g_down = nn.Linear(c.gate_rank, self.value_dim, bias=True)
+        self.decay_scale_log = nn.Parameter(torch.zeros(c.num_heads))
+        self.decay_bias = nn.Parameter(torch.zeros(self.value_dim))
+        self.o_norm = MemTRMSNormGated(c.head_dim, eps=c.norm_eps, output_gate_softcap_limit=c.output_softcap)
+        self.to(device=device, dtype=torch.bfloat16)
+        self.eval()
+
+    def _group_expand(self, latent, weight, gain):
+        """Per-group latent norm, then each group's up-projection
+        (models/deepseek/ops/compiled_tensor_ops.py:28-39)."""
+        groups, width, rank = weight.shape
+        inputs = _latent_norm(latent.reshape(-1, groups, rank), gain, self.norm_eps)
+        # bf16 bmm with both operands contiguous
+        out = torch.bmm(inputs.transpose(0, 1).contiguous(), weight.transpose(1, 2).contiguous())
+        return out.transpose(0, 1).reshape(*latent.shape[:-1], groups * width)
+
+    def _project(self, hidden_states):
+        """``(q, k, v, output_gate, erase, write, decay)`` raw projection rows
+        [1, T, H*D] bf16 (models/deepseek/layer.py:109-151; the gates are formed
+        by the prologue kernel)."""
+        parts = self.in_proj(hidden_states.unsqueeze(0)).split((*self.qkv_rows, *self.gate_rows), dim=-1)
+        q = F.linear(_latent_norm(parts[0], self.q_norm.weight, self.q_norm.eps), self.q_up.weight)
+        k = self._group_expand(parts[1], self.k_group_up, self.k_group_norm)
+        v = self._group_expand(parts[2], self.v_group_up, self.v_group_norm)
+        erase = F.linear(parts[3], self.b_up.weight)
+        write = F.linear(parts[4], self.w_up.weight)
+        decay = F.linear(parts[5], self.f_down.weight)
+        output_gate = F.linear(parts[6], self.g_down.weight, self.g_down.bias)
+        return q, k, v, output_gate, erase, write, decay
+
+    def _output(self, read, output_gate):
+        T = read.shape[1]
+        return self.o_norm(read.reshape(-1, self.head_dim), output_gate.reshape(-1, self.head_dim)).view(
+            T, self.value_dim)
+
+    @torch.no_grad()
+    def packed(self, hidden_states, read_states, *, lengths, commit, write_states):
+        """``(residual [T, H*D] bf16, next_state [N,H,D,D] fp32 | None)``
+        (models/deepseek/layer.py:153-183)."""
+        validate_packed_inputs(self, hidden_states, read_states, write_states, lengths)
+        T, H, D = len(hidden_states), self.num_heads, self.head_dim
+        q, k, v, output_gate, erase, write, decay = self._project(hidden_states)
+        if not commit:
+            q_hat = l2norm(q.reshape(1, T, H, D))
+            read = snapshot_read(q_hat, read_states, lengths, self.read_scale, bf16_accumulator_output=True)
+            return self._output(read, output_gate), None
+        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H,
+                                                eps=1e-6)
+        read, next_state = token_memory_packed_flash(
+            q_hat, k_til, v.reshape(1, T, H, D), g, beta, read_states, write_states, lengths=lengths,
+            scale=self.read_scale, chunk_tokens=self.chunk_tokens)
+        return self._output(read, output_gate), next_state
+
+    @torch.no_grad()
+    def packed_slots(self, hidden_states, pool, read_slot, write_slot, *, lengths, commit):
+        """``packed`` on a state pool in place (see ``QwenMemoryBlock.packed_slots``)."""
+        T, H, D = len(hidden_states), self.num_heads, self.head_dim
+        if hidden_states.ndim != 2 or hidden_states.shape[1] != self.hidden_size or \
+                hidden_states.dtype != torch.bfloat16 or not hidden_states.is_cuda:
+            raise ValueError("Memory expects CUDA BF16 hidden states [tokens, hidden_size]")
+        if not lengths or any(n <= 0 for n in lengths) or sum(lengths) != T:
+            raise ValueError("Packed sample lengths must cover the hidden token rows")
+        if pool.device != hidden_states.device or pool.dtype != torch.float32 or pool.shape[-3:] != (H, D, D):
+            raise ValueError(f"Memory expects an FP32 state pool [slots, ..., {H}, {D}, {D}] on the hidden device")
+        q, k, v, output_gate, erase, write, decay = self._project(hidden_states)
+        if not commit:
+            read = read_slots(l2norm(q.reshape(1, T, H, D)), pool, read_slot, lengths, self.read_scale)
+            return self._output(read, output_gate)
+        q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H,
+                                                eps=1e-6)
+        read = token_memory_packed_slots(q_hat, k_til, v.reshape(1, T, H, D), g, beta, pool, read_slot, write_slot,
+                                         erase=None, lengths=lengths, scale=self.read_scale,
+                                         chunk_tokens=self.chunk_tokens)
+        return self._output(read, output_gate)
+
+    def forward(self, hidden_states, initial_state, *, commit):
+        """Single-request entry (models/deepseek/layer.py:190-198)."""
         return self.packed(hidden_states, initial_state, lengths=[len(hidden_states)], commit=commit,
                            write_states=initial_state)

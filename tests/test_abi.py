@@ -81,6 +81,26 @@ def test_host_side_rejections(lib):
     assert extra >= 8 * 16 * 128 * 128 * 4 * 3
 
 
+def test_d512_modes(lib):
+    """d = 512 (the Flash head) takes the final-state and snapshot modes; the
+    causal output and the raw-projection entry point return EUNSUPPORTED
+    before any launch.  Its long sequences never take the two-level scan, so
+    the workspace holds the chunk records only."""
+    plan = _lib.Plan(n_chunk=0, n_seq=1, n_block=1)
+    call = lambda mode: lib.memt_gdn2_chunk_update(  # noqa: E731
+        None, None, None, None, None, 0, None, None, None, None, None, None, ctypes.byref(plan), 0, 1, 512, 512, 1.0,
+        mode, None, 0, None)
+    assert call(2) == _lib.EUNSUPPORTED
+    assert call(7) == _lib.EINVAL
+    x = _lib.Projections()
+    assert lib.memt_gdn2_chunk_update_fused(ctypes.byref(x), None, None, None, None, 0, None, None, None, None,
+                                            ctypes.byref(plan), 0, 1, 512, 512, 1.0, 0, None, 0,
+                                            None) == _lib.EUNSUPPORTED
+    ws = lib.memt_gdn2_chunk_update_workspace_size
+    assert ws(256, 1, 2, 512, 512, 1) == ws(256, 64, 2, 512, 512, 1)
+    assert ws(256, 1, 2, 256, 256, 1) > ws(256, 64, 2, 256, 256, 1)  # d = 256 does group
+
+
 def test_python_layer_fails_loudly_without_gpu():
     import torch
 
