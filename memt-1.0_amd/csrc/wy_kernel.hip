@@ -12,10 +12,11 @@
 // Outputs go to the workspace as MFMA operand fragments of the state scan
 // (P-frags for W, qg, kg^T and Aqk; a C-frag for U).
 //
-// Register layout.  Wave w owns tokens [16w, 16w+16).  Lane l holds token
-// 16w + l%16 and, for channel step s, the 8 channels
-//   slot j -> channel 32 s + 16 (j / 4) + 4 (l / 16) + j % 4      (P-frag order)
-// of every per-token input.  Loaded once in that order, the registers serve
+// Register layout.  The workgroup has one or two channel groups of 4 waves;
+// wave w of a group owns tokens [16w, 16w+16) over the group's channels.  Lane
+// l holds token 16w + l%16 and, for channel step s, the 8 channels
+//   slot j -> channel c0 + 32 s + 16 (j / 4) + 4 (l / 16) + j % 4      (P-frag order)
+// of every per-token input, c0 the group's first channel.  Loaded once in that order, the registers serve
 // directly as MFMA A operands of row-block products, as B operands of the
 // transposed products, and as P-frag records of the outputs.
 //
