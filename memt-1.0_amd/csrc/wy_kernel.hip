@@ -60,6 +60,8 @@ __device__ __forceinline__ f32x4 pick4(const float (&x)[16], int q) {
 // registers per wave (at most 128: two 8-wave workgroups per CU, 16 waves to
 // hide the load latency, against 8 with one group); d = 256 keeps 128 channels
 // per group, one workgroup per CU (its LDS).
+// (Four groups of 64 channels at d = 256, 16 waves in the one workgroup its LDS
+// allows per CU, measured no faster than two groups.)
 __host__ __device__ constexpr int wy_groups(int K) { return K >= 128 ? 2 : 1; }
 // waves per SIMD the register budget is sized for
 __host__ __device__ constexpr int wy_waves_per_simd(int K) { return K == 128 ? 4 : K < 128 ? 2 : 1; }
@@ -566,28 +568,35 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   }  // pass
   if constexpr (NCG > 1) {
     // sum the groups' partial tiles into group 0 (tiles J <= wave: 10 per group
-    // and matrix), through the off-diagonal operand buffer, dead once read
-    lds_barrier();
+    // and matrix), through the off-diagonal operand buffer, dead once read; FIT
+    // groups' tiles fit it at once, so more groups take several rounds
+    constexpr int PER_GROUP = 2 * 10 * 64 * 4;                // floats of one group's L and Aqk tiles
+    constexpr int FIT = (int)(sizeof(xch_s) / sizeof(float)) / PER_GROUP;
+    static_assert(FIT >= 1, "reduction buffer");
     float* red = (float*)xch_s;
-    auto slot = [&](int g2, int q2, int J) { return ((((g2 - 1) * 2 + q2) * 10 + wave * (wave + 1) / 2 + J) * 64 + lane) * 4; };
-    if (cg > 0) {
+    auto slot = [&](int idx, int q2, int J) { return (((idx * 2 + q2) * 10 + wave * (wave + 1) / 2 + J) * 64 + lane) * 4; };
 #pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        if (J > wave) continue;
-        *(f32x4*)(&red[slot(cg, 0, J)]) = Lt[J];
-        if constexpr (CAUSAL) *(f32x4*)(&red[slot(cg, 1, J)]) = Qt[J];
-      }
-    }
-    lds_barrier();
-    if (cg == 0) {
-#pragma unroll
-      for (int g2 = 1; g2 < NCG; ++g2)
+    for (int r0 = 1; r0 < NCG; r0 += FIT) {
+      lds_barrier();  // every wave is done with the buffer's previous contents
+      if (cg >= r0 && cg < r0 + FIT) {
 #pragma unroll
         for (int J = 0; J < 4; ++J) {
           if (J > wave) continue;
-          Lt[J] += *(const f32x4*)(&red[slot(g2, 0, J)]);
-          if constexpr (CAUSAL) Qt[J] += *(const f32x4*)(&red[slot(g2, 1, J)]);
+          *(f32x4*)(&red[slot(cg - r0, 0, J)]) = Lt[J];
+          if constexpr (CAUSAL) *(f32x4*)(&red[slot(cg - r0, 1, J)]) = Qt[J];
         }
+      }
+      lds_barrier();
+      if (cg == 0) {
+#pragma unroll
+        for (int g2 = r0; g2 < (r0 + FIT < NCG ? r0 + FIT : NCG); ++g2)
+#pragma unroll
+          for (int J = 0; J < 4; ++J) {
+            if (J > wave) continue;
+            Lt[J] += *(const f32x4*)(&red[slot(g2 - r0, 0, J)]);
+            if constexpr (CAUSAL) Qt[J] += *(const f32x4*)(&red[slot(g2 - r0, 1, J)]);
+          }
+      }
     }
   }
   // masks, the Aqk record, the inverse: group 0 (the other groups wait at the barriers)
