@@ -99,7 +99,7 @@ def bench_update(dev, steps, warmup, T=8192, H=16, D=128, out_mode="causal", on_
     import memt_gdn2
 
     nbytes_set = update_bytes(T, H, D, D)
-    nsets = max(2, int(np.ceil(2 * MALL_BYTES / nbytes_set)))
+    nsets = max(4, int(np.ceil(2 * MALL_BYTES / nbytes_set)))
     make = _inputs_on_device if on_device else _inputs
     sets = [make(T, H, D, D, seed=20261201 + i, dev=dev) for i in range(nsets)]
 
