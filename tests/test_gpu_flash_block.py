@@ -141,3 +141,33 @@ def test_flash_block_slots_match_packed(dev, commit):
     else:
         assert torch.equal(pool, before)
     assert torch.equal(pool[[0, 2]], before[[0, 2]])
+
+
+def test_flash_block_through_the_runtime(dev):
+    """The serving caller with the Flash block: the gather path and the slot
+    path give the same residual rows and slot states."""
+    from memt_gdn2.runtime import MemoryRequest, MemoryRuntime, plan_of
+
+    print("flash block through the runtime", flush=True)
+    cfg = _config()
+    block = _block(dev, cfg, seed=4)
+    g = torch.Generator(device=dev).manual_seed(8)
+    storage0 = torch.randn(5, 1, 2, 512, 512, generator=g, device=dev) * 0.05
+    plan = plan_of([(MemoryRequest("c1", "a", "commit"), 50), (MemoryRequest("q1", "b", "query"), 2),
+                    (MemoryRequest("c2", "d", "commit"), 70)])
+    slot_of = {"c1": 3, "q1": 0, "c2": 4}
+    hidden = torch.randn(plan.token_count, cfg.hidden_size, generator=g, device=dev).to(torch.bfloat16)
+    results = []
+    for slot_io in (False, True):
+        pool = types.SimpleNamespace(storage={0: storage0.clone()})
+        rt = MemoryRuntime(pool, slot_io=slot_io)
+        rt.begin(plan, slot_of=slot_of, memory_read={"a": True, "b": True, "d": True})
+        out = torch.empty(plan.token_count, block.value_dim, dtype=hidden.dtype, device=dev)  # [T, H*D] residual
+        rt.run_layer(0, hidden, out, block)
+        rt.finish(True)
+        torch.cuda.synchronize()
+        results.append((out, pool.storage[0]))
+    assert torch.equal(results[0][0], results[1][0])
+    assert torch.equal(results[0][1], results[1][1])
+    assert not torch.equal(results[1][1][3], storage0[3])  # the commits wrote their slots
+    assert torch.equal(results[1][1][:3], storage0[:3])
