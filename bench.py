@@ -414,7 +414,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "update (wy_kernel + state_kernel launches per step)",
+            "kernel": "update step: wy_kernel, trans_kernel, combine_kernel and state_kernel, timed together per step",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
