@@ -8,9 +8,9 @@ using namespace memt;
 namespace {
 
 bool supported_kv(int K, int V) { return K == V && (K == 64 || K == 128 || K == 256 || K == 512); }
-// d = 512 has no causal output and no raw-projection path (its model reads
-// memory through the snapshot read only)
-bool wide_ok(int K, bool causal, bool raw) { return K <= 256 || (!causal && !raw); }
+// d = 512 has no causal output (its model reads memory through the snapshot
+// read only)
+bool wide_ok(int K, bool causal) { return K <= 256 || !causal; }
 
 int status_of(hipError_t e) { return e == hipSuccess ? MEMT_GDN2_OK : MEMT_GDN2_ELAUNCH; }
 
@@ -139,7 +139,7 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   if (beta_dtype != MEMT_GDN2_F32 && beta_dtype != MEMT_GDN2_BF16) return MEMT_GDN2_EUNSUPPORTED;
   if (out_mode != MEMT_GDN2_OUT_NONE && out_mode != MEMT_GDN2_OUT_SNAPSHOT && out_mode != MEMT_GDN2_OUT_CAUSAL)
     return MEMT_GDN2_EINVAL;
-  if (!wide_ok(K, out_mode == MEMT_GDN2_OUT_CAUSAL, x != nullptr)) return MEMT_GDN2_EUNSUPPORTED;
+  if (!wide_ok(K, out_mode == MEMT_GDN2_OUT_CAUSAL)) return MEMT_GDN2_EUNSUPPORTED;
   if (plan->n_chunk > 0) {
     if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || plan->seq_chunk_offsets == nullptr)
       return MEMT_GDN2_EINVAL;
@@ -277,7 +277,7 @@ int memt_gdn2_wy_fwd(const void* q, const void* k, const void* v, const float* g
   if (plan->n_chunk > 0 && (k == nullptr || v == nullptr || gk == nullptr || beta == nullptr)) return MEMT_GDN2_EINVAL;
   if ((Aqk != nullptr || qg != nullptr) && q == nullptr) return MEMT_GDN2_EINVAL;
   const bool causal = q != nullptr;
-  if (!wide_ok(K, causal, false)) return MEMT_GDN2_EUNSUPPORTED;
+  if (!wide_ok(K, causal)) return MEMT_GDN2_EUNSUPPORTED;
   const WyLayout lay = wy_layout(plan->n_chunk, H, K, V, causal);
   if (plan->n_chunk > 0 && (workspace == nullptr || workspace_bytes < lay.total || ((uintptr_t)workspace & 255u)))
     return MEMT_GDN2_EWORKSPACE;

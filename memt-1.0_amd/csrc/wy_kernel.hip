@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   // d > 256 runs the channels in NP passes of KP (VP) channels, each in the d = 256 layout
   constexpr int NP = wy_passes(K), KP = K / NP, VP = V / NP, KSP = KS / NP, VSP = VS / NP;
   constexpr int KSL = KSP / NCG, VSL = VSP / NCG, KTL = 2 * KSL, VTL = 2 * VSL;  // per channel group and pass
-  static_assert(NP == 1 || (!CAUSAL && !RAW && K == V), "d > 256: no causal output, no raw projections");
+  static_assert(NP == 1 || (!CAUSAL && K == V), "d > 256: no causal output");
   constexpr int XP = C + 8;   // element pitch of the column-major xw / xu tiles
   constexpr int AP = C + 4;   // fp32 pitch of As_s
   constexpr int LQ = 16 + 4;  // fp32 pitch of a diagonal L tile
@@ -136,6 +136,42 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     for (int J = 0; J < 4; ++J) Lt[J] = Qt[J] = zero4();
   }
   f16x8 xw8[NP][KSL];  // xw rows of each pass, staged in LDS after the inverse
+  // d > 256 from raw projections: the l2 norms of q and k span both passes, so
+  // their sums come first (each pass reads its q and k again, from L2)
+  float sq_tot = 0.f, sk_tot = 0.f;
+  if constexpr (RAW && NP > 1) {
+    const size_t tr = (size_t)(tok0 + (valid ? t : 0));
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int s = 0; s < KSL; ++s)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int c0 = h * K + p * KP + cbl + 32 * s + 16 * half + 4 * lg;
+          const bf16x4 qq = *(const bf16x4*)(a.q + tr * a.q_stride + c0);
+          const bf16x4 kk = *(const bf16x4*)(a.k + tr * a.k_stride + c0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sq_tot += (float)qq[e] * (float)qq[e];
+            sk_tot += (float)kk[e] * (float)kk[e];
+          }
+        }
+    sq_tot += __shfl_xor(sq_tot, 16, 64);
+    sq_tot += __shfl_xor(sq_tot, 32, 64);
+    sk_tot += __shfl_xor(sk_tot, 16, 64);
+    sk_tot += __shfl_xor(sk_tot, 32, 64);
+    if (lg == 0) {
+      nrm_s[(cg * C + t) * 2] = sq_tot;
+      nrm_s[(cg * C + t) * 2 + 1] = sk_tot;
+    }
+    lds_barrier();
+    sq_tot = sk_tot = 0.f;
+#pragma unroll
+    for (int c2 = 0; c2 < NCG; ++c2) {
+      sq_tot += nrm_s[(c2 * C + t) * 2];
+      sk_tot += nrm_s[(c2 * C + t) * 2 + 1];
+    }
+  }
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int cb = p * KP + cbl, vcb = p * VP + vcbl;  // global channel / value column of this pass
@@ -168,14 +204,16 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
           }
         }
       asm volatile("" ::: "memory");
+      if constexpr (NP == 1) {  // d > 256 loads v and the write gate for the U product only
 #pragma unroll
-      for (int s = 0; s < VSL; ++s)
+        for (int s = 0; s < VSL; ++s)
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int c0 = h * V + vcb + 32 * s + 16 * half + 4 * lg;
-          vraw[s][half] = *(const bf16x4*)(a.v + tr * a.v_stride + c0);
-          btraw[s][half] = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + c0);
-        }
+          for (int half = 0; half < 2; ++half) {
+            const int c0 = h * V + vcb + 32 * s + 16 * half + 4 * lg;
+            vraw[s][half] = *(const bf16x4*)(a.v + tr * a.v_stride + c0);
+            btraw[s][half] = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + c0);
+          }
+      }
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int s = 0; s < KSL; ++s)
@@ -343,20 +381,22 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     if constexpr (RAW) {
       // q_hat = bf16(q / sqrt(sum q^2 + eps)), k_til = bf16(sqrt_b * bf16(k / sqrt(sum k^2 + eps)))
       // with sqrt_b = bf16(exp(logsigmoid(e) / 2)); a token's channels sit on the four lanes lr + 16 i
-      float sq = 0.f, sk = 0.f;
+      float sq = sq_tot, sk = sk_tot;  // d > 256: both passes' sums, from before the loop
+      if constexpr (NP == 1) {
 #pragma unroll
-      for (int s = 0; s < KSL; ++s)
+        for (int s = 0; s < KSL; ++s)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float qv = (float)qraw[s][j], kv = (float)kraw[s][j];
-          sq += qv * qv;
-          sk += kv * kv;
-        }
-      sq += __shfl_xor(sq, 16, 64);
-      sq += __shfl_xor(sq, 32, 64);
-      sk += __shfl_xor(sk, 16, 64);
-      sk += __shfl_xor(sk, 32, 64);
-      if constexpr (NCG > 1) {
+          for (int j = 0; j < 8; ++j) {
+            const float qv = (float)qraw[s][j], kv = (float)kraw[s][j];
+            sq += qv * qv;
+            sk += kv * kv;
+          }
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        sk += __shfl_xor(sk, 16, 64);
+        sk += __shfl_xor(sk, 32, 64);
+      }
+      if constexpr (NCG > 1 && NP == 1) {
         // each group holds K / NCG of the token's channels
         if (lg == 0) {
           nrm_s[(cg * C + t) * 2] = sq;
@@ -673,16 +713,27 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     }
     if constexpr (NP > 1) {
       const int vcb = p * VP + vcbl;
+      const size_t tr = (size_t)(tok0 + (valid ? t : 0));
 #pragma unroll
       for (int s = 0; s < VSL; ++s) {
         f16x8 xu8;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
-          const bf16x4 v4 = *(const bf16x4*)(a.v + rowV + c0);
-          const BetaRaw b4 = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+          bf16x4 v4;
+          BetaRaw b4;
+          if constexpr (RAW) {  // projection rows; beta = bf16(sigmoid(write logit))
+            v4 = *(const bf16x4*)(a.v + tr * a.v_stride + h * V + c0);
+            b4 = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + h * V + c0);
+          } else {
+            v4 = *(const bf16x4*)(a.v + rowV + c0);
+            b4 = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+          }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) xu8[4 * half + e] = (_Float16)(valid ? (float)v4[e] * (float)b4[e] : 0.f);
+          for (int e = 0; e < 4; ++e) {
+            const float bt = RAW ? (float)(__bf16)sigmoid_bf16((float)b4[e]) : (float)b4[e];
+            xu8[4 * half + e] = (_Float16)(valid ? (float)v4[e] * bt : 0.f);
+          }
         }
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -815,7 +866,8 @@ hipError_t launch_kv(const WyArgs& a, int n_chunk, bool causal, bool g_cum, bool
   const bool has_b = a.b != nullptr;
   if constexpr (wy_passes(K) > 1) {
     // d > 256: the final-state and snapshot-read modes only
-    if (causal || a.f_raw != nullptr) return hipErrorInvalidValue;
+    if (causal) return hipErrorInvalidValue;
+    if (a.f_raw != nullptr) return launch_raw<K, V, false>(a, n_chunk, stream);
     if (g_cum) return has_b ? launch_t<K, V, false, true, true>(a, n_chunk, beta_bf16, stream)
                             : launch_t<K, V, false, false, true>(a, n_chunk, beta_bf16, stream);
     return has_b ? launch_t<K, V, false, true, false>(a, n_chunk, beta_bf16, stream)

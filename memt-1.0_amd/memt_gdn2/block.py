@@ -14,8 +14,9 @@ GEMMs (hipBLASLt).  Everything after them runs in this package's kernels:
 
 ``DeepSeekMemoryBlock`` does the same for the Flash model
 (models/deepseek/layer.py:46-183): grouped low-rank Q/K/V and gate
-projections in torch, then the prologue kernel, ``token_memory_packed_flash``
-(or the snapshot read for queries) and the gated RMSNorm, at d = 512.
+projections in torch, then the update with the prologue inside its WY kernel
+(or the prologue kernel and ``token_memory_packed_flash``), or the snapshot
+read for queries, and the gated RMSNorm, at d = 512.
 """
 
 from __future__ import annotations
@@ -173,8 +174,9 @@ class DeepSeekMemoryBlock(nn.Module):
     ``output_softcap``.  Every token reads the incoming state; a commit also
     returns the final state."""
 
-    def __init__(self, memory_config, *, device=None):
+    def __init__(self, memory_config, *, device=None, fused_prologue: bool = True):
         super().__init__()
+        self.fused_prologue = fused_prologue
         c = memory_config
         self.hidden_size = c.hidden_size
         self.num_heads = c.num_heads
@@ -243,6 +245,11 @@ class DeepSeekMemoryBlock(nn.Module):
             q_hat = l2norm(q.reshape(1, T, H, D))
             read = snapshot_read(q_hat, read_states, lengths, self.read_scale, bf16_accumulator_output=True)
             return self._output(read, output_gate), None
+        if self.fused_prologue:
+            read, next_state = token_memory_packed_fused(
+                q, k, v, decay, self.decay_bias, self.decay_scale_log, erase, write, read_states, write_states,
+                lengths=lengths, scale=self.read_scale, chunk_tokens=self.chunk_tokens, num_heads=H)
+            return self._output(read, output_gate), next_state
         q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H,
                                                 eps=1e-6)
         read, next_state = token_memory_packed_flash(
@@ -264,6 +271,11 @@ class DeepSeekMemoryBlock(nn.Module):
         q, k, v, output_gate, erase, write, decay = self._project(hidden_states)
         if not commit:
             read = read_slots(l2norm(q.reshape(1, T, H, D)), pool, read_slot, lengths, self.read_scale)
+            return self._output(read, output_gate)
+        if self.fused_prologue:
+            read = token_memory_packed_fused_slots(
+                q, k, v, decay, self.decay_bias, self.decay_scale_log, erase, write, pool, read_slot, write_slot,
+                lengths=lengths, scale=self.read_scale, chunk_tokens=self.chunk_tokens, num_heads=H)
             return self._output(read, output_gate)
         q_hat, k_til, beta, g = memory_prologue(q, k, decay, self.decay_bias, self.decay_scale_log, erase, write, H,
                                                 eps=1e-6)

@@ -82,10 +82,10 @@ def test_host_side_rejections(lib):
 
 
 def test_d512_modes(lib):
-    """d = 512 (the Flash head) takes the final-state and snapshot modes; the
-    causal output and the raw-projection entry point return EUNSUPPORTED
-    before any launch.  Its long sequences never take the two-level scan, so
-    the workspace holds the chunk records only."""
+    """d = 512 (the Flash head) takes the final-state and snapshot modes, also
+    from raw projections; the causal output returns EUNSUPPORTED before any
+    launch.  Its long sequences never take the two-level scan, so the
+    workspace holds the chunk records only."""
     plan = _lib.Plan(n_chunk=0, n_seq=1, n_block=1)
     call = lambda mode: lib.memt_gdn2_chunk_update(  # noqa: E731
         None, None, None, None, None, 0, None, None, None, None, None, None, ctypes.byref(plan), 0, 1, 512, 512, 1.0,
@@ -94,7 +94,7 @@ def test_d512_modes(lib):
     assert call(7) == _lib.EINVAL
     x = _lib.Projections()
     assert lib.memt_gdn2_chunk_update_fused(ctypes.byref(x), None, None, None, None, 0, None, None, None, None,
-                                            ctypes.byref(plan), 0, 1, 512, 512, 1.0, 0, None, 0,
+                                            ctypes.byref(plan), 0, 1, 512, 512, 1.0, 2, None, 0,
                                             None) == _lib.EUNSUPPORTED
     ws = lib.memt_gdn2_chunk_update_workspace_size
     assert ws(256, 1, 2, 512, 512, 1) == ws(256, 64, 2, 512, 512, 1)

@@ -202,7 +202,7 @@ def test_runtime_step_on_gpu_slots(dev):
     assert torch.equal(pool.storage[0][:4], before[:4])
 
 
-@pytest.mark.parametrize("D,lengths", [(128, [150, 1, 300]), (64, [40, 700]), (256, [90, 130])])
+@pytest.mark.parametrize("D,lengths", [(128, [150, 1, 300]), (64, [40, 700]), (256, [90, 130]), (512, [70, 1, 100])])
 def test_fused_prologue_update(dev, D, lengths):
     """The update from raw projections (prologue in the WY kernel) against the
     prologue kernel followed by token_memory_packed, and against the oracle;

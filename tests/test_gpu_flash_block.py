@@ -1,8 +1,9 @@
 """GPU parity of the Flash memory block (models/deepseek/layer.py:46-183) at
 d = 512: its grouped low-rank projections against an fp64 restatement of the
 reference's projection code (models/deepseek/ops/compiled_tensor_ops.py:12-99),
-and ``packed`` (query and commit) against the oracle run on the block's own
-bf16 projection outputs; ``packed_slots`` must equal ``packed`` bit for bit."""
+and ``packed`` (query and commit, with the prologue inside the update's WY
+kernel or as its own kernel) against the oracle run on the block's own bf16
+projection outputs; ``packed_slots`` must equal ``packed`` bit for bit."""
 
 import types
 
@@ -26,9 +27,9 @@ def _config(**kw):
     return types.SimpleNamespace(**base)
 
 
-def _block(dev, cfg, seed=0):
+def _block(dev, cfg, seed=0, fused=True):
     torch.manual_seed(seed)
-    block = DeepSeekMemoryBlock(cfg, device=dev)
+    block = DeepSeekMemoryBlock(cfg, device=dev, fused_prologue=fused)
     with torch.no_grad():
         for name, p in block.named_parameters():
             if name.endswith("norm.weight") or name.endswith("group_norm"):
@@ -98,11 +99,12 @@ def _oracle_packed(block, hidden, read_states, lengths, commit, write_states):
     return out.reshape(T, H * D), final
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("commit", [False, True])
-def test_flash_block_packed(dev, commit):
-    print(f"flash block packed commit={commit}", flush=True)
+def test_flash_block_packed(dev, commit, fused):
+    print(f"flash block packed commit={commit} fused={fused}", flush=True)
     cfg = _config()
-    block = _block(dev, cfg, seed=2)
+    block = _block(dev, cfg, seed=2, fused=fused)
     lengths = [70, 1, 90]
     T = sum(lengths)
     g = torch.Generator(device=dev).manual_seed(5)
@@ -119,11 +121,12 @@ def test_flash_block_packed(dev, commit):
         assert final is None
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("commit", [False, True])
-def test_flash_block_slots_match_packed(dev, commit):
-    print(f"flash block slots commit={commit}", flush=True)
+def test_flash_block_slots_match_packed(dev, commit, fused):
+    print(f"flash block slots commit={commit} fused={fused}", flush=True)
     cfg = _config()
-    block = _block(dev, cfg, seed=3)
+    block = _block(dev, cfg, seed=3, fused=fused)
     lengths = [40, 100]
     T = sum(lengths)
     g = torch.Generator(device=dev).manual_seed(6)
