@@ -196,7 +196,9 @@ int memt_gdn2_chunk_update_slots(const void* q, const void* k, const void* v, co
  * (required for out_mode SNAPSHOT, which reads it).  States as in
  * memt_gdn2_chunk_update, or, when h0_slot / ht_slot (and read_slot) are not
  * NULL, a pool of n_slots states addressed as in memt_gdn2_chunk_update_slots
- * (h0, ht and read_states then name the same pool).
+ * (h0, ht and read_states then name the same pool).  Also the Flash block's
+ * commit (models/deepseek/layer.py:153-183, the same gate and q/k formulas)
+ * at K = V = 512, without the causal output.
  */
 int memt_gdn2_chunk_update_fused(const memt_gdn2_projections* x, void* q_hat, const float* h0, float* ht,
                                  const float* read_states, int n_slots, const int32_t* read_slot,
