@@ -89,7 +89,7 @@ template <int K, int V, bool CAUSAL, bool HAS_B, bool G_CUM, typename BetaT, boo
 __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_kernel(WyArgs a) {
   static_assert(!RAW || (!HAS_B && !G_CUM), "raw projections carry the erase gate in k and g un-summed");
   constexpr int C = kChunk;
-  constexpr int KS = K / 32, VS = V / 32, KT = K / 16, VT = V / 16;  // whole-head counts (record layouts)
+  constexpr int KS = K / 32, VS = V / 32, VT = V / 16;  // whole-head counts (record layouts)
   constexpr int NCG = wy_groups(K), NT = 256 * NCG;
   // d > 256 runs the channels in NP passes of KP (VP) channels, each in the d = 256 layout
   constexpr int NP = wy_passes(K), KP = K / NP, VP = V / NP, KSP = KS / NP, VSP = VS / NP;
@@ -172,6 +172,8 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       sk_tot += nrm_s[(c2 * C + t) * 2 + 1];
     }
   }
+  // (at d = 512 the compiler declines the full unroll for size and keeps the
+  // loop with xw8 in registers; forcing it measured slightly slower)
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int cb = p * KP + cbl, vcb = p * VP + vcbl;  // global channel / value column of this pass
@@ -611,7 +613,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     // and matrix), through the off-diagonal operand buffer, dead once read; FIT
     // groups' tiles fit it at once, so more groups take several rounds
     constexpr int PER_GROUP = 2 * 10 * 64 * 4;                // floats of one group's L and Aqk tiles
-    constexpr int FIT = (int)(sizeof(xch_s) / sizeof(float)) / PER_GROUP;
+    constexpr int FIT = (int)(XCH * sizeof(_Float16) / sizeof(float)) / PER_GROUP;
     static_assert(FIT >= 1, "reduction buffer");
     float* red = (float*)xch_s;
     auto slot = [&](int idx, int q2, int J) { return (((idx * 2 + q2) * 10 + wave * (wave + 1) / 2 + J) * 64 + lane) * 4; };
@@ -629,13 +631,15 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       lds_barrier();
       if (cg == 0) {
 #pragma unroll
-        for (int g2 = r0; g2 < (r0 + FIT < NCG ? r0 + FIT : NCG); ++g2)
+        for (int i = 0; i < FIT; ++i) {
+          if (r0 + i >= NCG) continue;
 #pragma unroll
           for (int J = 0; J < 4; ++J) {
             if (J > wave) continue;
-            Lt[J] += *(const f32x4*)(&red[slot(g2 - r0, 0, J)]);
-            if constexpr (CAUSAL) Qt[J] += *(const f32x4*)(&red[slot(g2 - r0, 1, J)]);
+            Lt[J] += *(const f32x4*)(&red[slot(i, 0, J)]);
+            if constexpr (CAUSAL) Qt[J] += *(const f32x4*)(&red[slot(i, 1, J)]);
           }
+        }
       }
     }
   }
