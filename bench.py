@@ -5,7 +5,9 @@ throughput (tokens/s) on the Nano-like single layer: B=1, H=16, T=8192,
 dk=dv=128, 64-token chunks, bf16 q/k/v, fp32 g/beta, fp32 initial state,
 causal chunk output (bf16) plus final state (fp32).  The same line carries
 the decode readout (batch 64 sequences, H=16, d=128, fused RMSNorm + output
-gate) in GB/s, the roofline of each, and the CPU baseline timed on the host.
+gate) in GB/s, the roofline of each, the roofs measured on the GPU (streaming
+read, device copy, an MFMA loop and a library GEMM) and the CPU baseline
+timed on the host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -269,6 +271,79 @@ def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8):
     }
 
 
+def _roofs_lib():
+    """The benchmark's roof probes (memt-1.0_amd/csrc/roofs.hip), built beside the library."""
+    import ctypes
+
+    path = ROOT / "memt-1.0_amd" / "memt_gdn2" / "libmemt_roofs.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: build it with `python memt-1.0_amd/memt_gdn2/_build.py`")
+    lib = ctypes.CDLL(os.fspath(path))
+    lib.memt_roofs_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.memt_roofs_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+MFMA_PROBE_CHAINS = 8        # independent MFMA chains per wave in roofs.hip
+MFMA_PROBE_FLOP = 16 * 16 * 32 * 2  # one v_mfma_f32_16x16x32_bf16
+
+
+def measured_roofs(dev, reps=20):
+    """Roofs measured on this GPU, reported beside the spec peaks: a device
+    copy of COPY_BYTES (reads and writes that many bytes), a streaming read of
+    the same bytes and a dense bf16 MFMA loop (both hand-written probes), and
+    a bf16 8192^3 GEMM through torch.mm (hipBLASLt)."""
+    lib = _roofs_lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    x = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
+    y = torch.empty_like(x)
+    copy_ms = _event_ms(lambda: y.copy_(x), reps, warmup=3)
+    del y
+    blocks = 2048
+    part = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+
+    def read():
+        if lib.memt_roofs_read(x.data_ptr(), COPY_BYTES, part.data_ptr(), blocks, stream) != 0:
+            raise RuntimeError("read probe launch failed")
+
+    read_ms = _event_ms(read, reps, warmup=3)
+    del x
+    iters = 2048
+
+    def mfma():
+        if lib.memt_roofs_mfma(part.data_ptr(), blocks, iters, stream) != 0:
+            raise RuntimeError("MFMA probe launch failed")
+
+    mfma_ms = _event_ms(mfma, reps, warmup=3)
+    n = 8192
+    a = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    b = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
+    gemm_ms = _event_ms(lambda: torch.mm(a, b, out=c), reps, warmup=3)
+    del a, b, c, part
+    torch.cuda.empty_cache()
+    copy_gbs = 2 * COPY_BYTES / (copy_ms * 1e-3) / 1e9
+    read_gbs = COPY_BYTES / (read_ms * 1e-3) / 1e9
+    mfma_tflops = blocks * 4 * MFMA_PROBE_CHAINS * iters * MFMA_PROBE_FLOP / (mfma_ms * 1e-3) / 1e12
+    gemm_tflops = 2 * n ** 3 / (gemm_ms * 1e-3) / 1e12
+    return {
+        "hbm_read_gbs": read_gbs,
+        "hbm_read_frac_of_spec": read_gbs / HBM_PEAK_GBS,
+        "hbm_read_workload": f"streaming read of {COPY_BYTES >> 30} GiB (16-byte non-temporal loads, "
+                             f"{blocks} x 256 threads), mean of {reps}",
+        "hbm_copy_gbs": copy_gbs,
+        "hbm_copy_frac_of_spec": copy_gbs / HBM_PEAK_GBS,
+        "hbm_copy_workload": f"torch device copy of {COPY_BYTES >> 30} GiB fp32 (read + write), mean of {reps}",
+        "mfma_bf16_tflops": mfma_tflops,
+        "mfma_bf16_frac_of_spec": mfma_tflops / MFMA_BF16_PEAK_TFLOPS,
+        "mfma_bf16_workload": f"v_mfma_f32_16x16x32_bf16 loop, {MFMA_PROBE_CHAINS} chains x {iters} per wave, "
+                              f"{blocks * 4} waves, mean of {reps}",
+        "gemm_bf16_tflops": gemm_tflops,
+        "gemm_bf16_frac_of_spec": gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
+        "gemm_bf16_workload": f"torch.mm bf16 {n}x{n}x{n} (hipBLASLt), mean of {reps}",
+    }
+
+
 def calibrate(dev, T=8192, H=16, D=128, reps=3):
     """Workload for hardware-counter runs (rocprofv3 --pmc): a device copy of
     COPY_BYTES (the reference for FETCH_SIZE / WRITE_SIZE per byte), then `reps`
@@ -380,6 +455,7 @@ def main():
         print(json.dumps(bench_flash(dev, args.steps, args.warmup)))
         return
 
+    roofs = measured_roofs(dev, reps=50)  # first: its 0.2 s of probes and GEMMs also brings the clocks up
     up = bench_update(dev, args.steps, args.warmup, T, H, D, out_mode=args.mode)
     snap = (bench_update(dev, max(10, args.steps // 2), args.warmup, T, H, D, out_mode="snapshot")
             if args.mode == "causal" else None)
@@ -441,6 +517,10 @@ def main():
         },
     }
     result["memory_block_commit"] = pro
+    result["measured_roofs"] = roofs
+    result["roofline"]["frac_of_measured_read"] = achieved / roofs["hbm_read_gbs"]
+    result["roofline"]["mfma_frac_of_measured"] = uf / t_up / 1e12 / roofs["mfma_bf16_tflops"]
+    result["readout"]["roofline"]["frac_of_measured_read"] = ro["gbs"] / roofs["hbm_read_gbs"]
     if snap is not None:
         result["snapshot_mode"] = {
             "workload": "token_memory_packed semantics (tokens read the incoming state), same shapes",

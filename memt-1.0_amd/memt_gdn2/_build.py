@@ -2,7 +2,9 @@
 
 Run as ``python memt-1.0_amd/memt_gdn2/_build.py`` or call :func:`build`.
 Objects go to ``memt-1.0_amd/_build/``; the shared library is written next
-to this file so it is found in-tree.
+to this file so it is found in-tree.  The same call builds
+``libmemt_roofs.so`` (the benchmark's read and MFMA roof probes, which the
+package never loads).
 """
 
 from __future__ import annotations
@@ -22,6 +24,8 @@ LIB_NAME = "libmemt_gdn2.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
 SOURCES = ["abi.hip", "wy_kernel.hip", "state_kernel.hip", "misc_kernels.hip", "prologue_kernel.hip", "plan.cpp"]
+ROOFS_SOURCE = "roofs.hip"
+ROOFS_PATH = PKG_DIR / "libmemt_roofs.so"
 
 # -packed-fp32-ops off: hipcc must not emit packed fp32 VALU ops for this code.
 HIPCC_FLAGS = [
@@ -66,13 +70,16 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
         cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    roofs_obj = BUILD_DIR / (Path(ROOFS_SOURCE).stem + ".o")
+    cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / ROOFS_SOURCE), "-o", str(roofs_obj)])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         for msg in ex.map(_run, cmds):
             if verbose and msg:
                 print(msg, file=sys.stderr)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
-    os.replace(tmp, LIB_PATH)
+    for out, inputs in ((LIB_PATH, objs), (ROOFS_PATH, [roofs_obj])):
+        tmp = out.with_suffix(".so.tmp")
+        _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, inputs), "-o", str(tmp)])
+        os.replace(tmp, out)
     return LIB_PATH
 
 
