@@ -133,11 +133,12 @@ struct GroupBuffers {
   float* S0;     // [n_group_bound, H, K, V] C-frag order, state entering each group
 };
 
-// State columns one scan workgroup carries: all of them up to d = 128; at
-// d = 256 a 64-column slice and at d = 512 a 32-column slice, so that the
-// K x slice fp32 state and the prefetched chunk records fit the registers of
-// two waves per SIMD.
-__host__ __device__ constexpr int scan_slice(int D) { return D > 256 ? 32 : D > 128 ? 64 : D; }
+// State columns one scan workgroup carries: all of them up to d = 128, and a
+// 64-column slice at d = 256 and d = 512, so that the K x slice fp32 state and
+// the prefetched chunk records fit the registers of two waves per SIMD (at
+// d = 512 with a 60-byte spill; 32-column slices, without it, ran 12-16 %
+// slower: twice the workgroups, each reading the head's full W and kg^T).
+__host__ __device__ constexpr int scan_slice(int D) { return D > 128 ? 64 : D; }
 
 // Chunks per group for the two-level scan (0 = plain per-sequence scan).
 // The scan runs one workgroup per (sequence or group, head, column slice).

@@ -2,8 +2,8 @@
 //
 // One workgroup (8 waves) per (sequence or chunk group, head, column slice)
 // holds a K x NC slice of the head's fp32 state in MFMA accumulators (all V
-// columns up to d = 128, 64-column slices at d = 256, 32-column slices at
-// d = 512) and walks the chunks in order (models/qwen/ops/_triton/state.py:76-115):
+// columns up to d = 128, 64-column slices at d = 256 and d = 512) and walks
+// the chunks in order (models/qwen/ops/_triton/state.py:76-115):
 //
 //   snapshot S if the chunk starts a read block
 //   V_new = U - W . f16(S)                         (erase path)
