@@ -9,7 +9,9 @@ namespace {
 // o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32 accumulation.
 // A workgroup takes CB state columns (all of them up to d = 256) of one head
 // for a run of `per` consecutive chunks, and reloads the bf16 state tile only
-// when the block changes.  Wave w handles token rows [16w, 16w + 16).
+// when the block changes.  Wave w handles token rows [16w, 16w + 16); it
+// issues all of a chunk's q loads before its first product, so a chunk costs
+// one memory latency rather than one per 32 channels.
 // With several column tiles (d = 512), the NCB workgroups of one (run, head)
 // read the same q rows: their block indices are 8 apart, so they share an XCD
 // (blocks go to the eight XCDs round-robin) and run together, and q comes from
@@ -41,33 +43,53 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
     const int blk = block_ids[chunk];
     if (blk != loaded) {
       if (loaded >= 0) __syncthreads();  // every wave is done with the previous tile
+      // NL 16-byte loads per thread, issued in batches of up to 16 ahead of
+      // their conversions, so a batch costs one memory latency
       const float* Sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V + col0;
-      for (int idx = tid; idx < K * CB / 4; idx += 256) {
-        const int row = idx / (CB / 4), c4 = (idx % (CB / 4)) * 4;
-        const f32x4 s4 = *(const f32x4*)(Sp + (size_t)row * V + c4);
+      constexpr int NL = K * CB / 4 / 256, BATCH = NL < 8 ? NL : 8;
+      static_assert(NL * 256 * 4 == K * CB && NL % BATCH == 0, "state tile split");
+#pragma unroll 1
+      for (int j0 = 0; j0 < NL; j0 += BATCH) {
+        f32x4 s4[BATCH];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S_lds[(c4 + e) * SKP + row] = (__bf16)s4[e];
+        for (int j = 0; j < BATCH; ++j) {
+          const int idx = tid + 256 * (j0 + j);
+          s4[j] = *(const f32x4*)(Sp + (size_t)(idx / (CB / 4)) * V + (idx % (CB / 4)) * 4);
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j) {
+          const int idx = tid + 256 * (j0 + j);
+          const int row = idx / (CB / 4), c4 = (idx % (CB / 4)) * 4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) S_lds[(c4 + e) * SKP + row] = (__bf16)s4[j][e];
+        }
       }
       __syncthreads();
       loaded = blk;
     }
+    // All K/32 q operands of this lane's row are loaded before the first
+    // product, so the chunk pays one memory latency.  Rows past the chunk end
+    // read its last row (they feed only output rows that are not stored); an
+    // empty chunk loads nothing.
     const int t = 16 * w + lr;
+    bf16x8 qa[K / 32];
+    if (len > 0) {
+      const __bf16* qp = q + ((size_t)(tok0 + min(t, len - 1)) * H + h) * K + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) qa[s] = *(const bf16x8*)(qp + 32 * s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) qa[s] = bf16x8{};
+    }
     f32x4 acc[CB / 16];
 #pragma unroll
     for (int ct = 0; ct < CB / 16; ++ct) acc[ct] = zero4();
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) {
-      bf16x8 qa;
-      if (t < len) {
-        qa = *(const bf16x8*)(q + ((size_t)(tok0 + t) * H + h) * K + 32 * s + 8 * lg);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qa[e] = (__bf16)0.f;
-      }
 #pragma unroll
       for (int ct = 0; ct < CB / 16; ++ct) {
         const bf16x8 sb = *(const bf16x8*)(&S_lds[(16 * ct + lr) * SKP + 32 * s + 8 * lg]);
-        acc[ct] = mfma_bf16(qa, sb, acc[ct]);
+        acc[ct] = mfma_bf16(qa[s], sb, acc[ct]);
       }
     }
 #pragma unroll
