@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
     const int blk = block_ids[chunk];
     if (blk != loaded) {
       if (loaded >= 0) __syncthreads();  // every wave is done with the previous tile
-      // NL 16-byte loads per thread, issued in batches of up to 16 ahead of
+      // NL 16-byte loads per thread, issued in batches of up to 8 ahead of
       // their conversions, so a batch costs one memory latency
       const float* Sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V + col0;
       constexpr int NL = K * CB / 4 / 256, BATCH = NL < 8 ? NL : 8;
