@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import gdn2 as O
-from gpu_util import bf, host, to_dev
+from gpu_util import bf, check, host, to_dev
 
 import memt_gdn2
 
@@ -31,7 +31,7 @@ def test_readout_fused(dev, B, H, D, gate_kind):
     out = memt_gdn2.readout_fused(to_dev(S, dev), bf(q, dev), bf(gate, dev), bf(w, dev), scale=D ** -0.5,
                                   eps=1e-6, gate_kind=gate_kind)
     ref = O.readout_fused(S, q, gate, w, scale=D ** -0.5, eps=1e-6, gate_kind=gate_kind).reshape(B, H * D)
-    assert O.parity_err(host(out), ref, out_bf16=True) <= TOL
+    check(f"readout B={B} H={H} D={D} {gate_kind}", host(out), ref, out_bf16=True)
 
 
 def test_readout_slot_indexed(dev):

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import gdn2 as O
-from gpu_util import bf, host, to_dev
+from gpu_util import bf, check, host, to_dev
 
 import memt_gdn2
 
@@ -136,12 +136,12 @@ def test_wide_state_full_workload(dev):
     o, ht = memt_gdn2.chunk_gdn2(q, k, v, g, beta, initial_state=h0, out_mode="causal")
     torch.cuda.synchronize()
     assert bool(torch.isfinite(o.float()).all()) and bool(torch.isfinite(ht).all())
-    hs = [7, 50]
+    hs = list(range(0, H, 9))  # 8 of the 64 heads (the fp64 oracle at d=256 costs ~1 s per head)
     sl = lambda t: t[0, :, hs].double().cpu()  # noqa: E731
     o_ref, h_ref = chunked_gdn2_torch(sl(q), sl(k), sl(v), sl(g), sl(beta), h0=h0[0, hs].double().cpu(),
                                       out_mode="causal", dtype=torch.float64)
-    assert O.max_rel_err(host(ht[0, hs]), h_ref.numpy()) <= TOL
-    assert O.parity_err(host(o[0, :, hs]), o_ref.numpy(), out_bf16=True) <= TOL
+    check(f"final state (heads {hs})", host(ht[0, hs]), h_ref.numpy(), out_bf16=False)
+    check("causal output (same heads)", host(o[0, :, hs]), o_ref.numpy(), out_bf16=True)
 
     B = 32
     states = torch.cat([ht, torch.randn(B - 1, H, D, D, generator=gen, device=dev) * 0.02])
@@ -150,4 +150,4 @@ def test_wide_state_full_workload(dev):
     wn = (1 + 0.1 * torch.randn(D, generator=gen, device=dev)).to(torch.bfloat16)
     out = memt_gdn2.readout_fused(states, qd, gate, wn, scale=D ** -0.5, eps=1e-6)
     ref = O.readout_fused(host(states), host(qd), host(gate), host(wn), scale=D ** -0.5, eps=1e-6)
-    assert O.parity_err(host(out), ref.reshape(B, H * D), out_bf16=True) <= TOL
+    check("batch-32 readout", host(out), ref.reshape(B, H * D), out_bf16=True)

@@ -40,6 +40,31 @@ def test_bf16_round_matches_torch():
     assert np.array_equal(O.bf16_round(x), ref)
 
 
+def test_parity_metric():
+    """The asserted metric allows exactly the output format's half-ulp rounding:
+    a correctly rounded bf16 copy of the reference scores 0, one more ulp
+    scores half an ulp; the plain max-relative error and the floored
+    elementwise p99 follow their definitions on a hand-built case."""
+    rng = _rng(11)
+    ref = rng.standard_normal(4096) * 3.0
+    xr = O.bf16_round(ref).astype(np.float64)
+    assert O.parity_err(xr, ref, out_bf16=True) == 0.0
+    assert O.parity_err(xr, ref, out_bf16=False) > 0.0
+    up = xr + O.bf16_ulp(xr) * np.sign(xr - ref + 1e-300)  # one more ulp away from ref
+    den = np.max(np.abs(ref))
+    got = O.parity_err(up, ref, out_bf16=True)
+    assert got >= 0.5 * np.min(O.bf16_ulp(ref[np.abs(ref) > 1.0])) / den * 0.99
+    ref2 = np.array([10.0, 1.0, 0.0, -5.0] * 25)
+    x2 = ref2.copy()
+    x2[1] = 1.5  # one element off by 0.5: |d| / |ref| = 0.5, |d| / max = 0.05
+    r = O.parity_report(x2, ref2, out_bf16=False)
+    assert r["max_rel"] == pytest.approx(0.05) and r["parity"] == pytest.approx(0.05)
+    # 1 of 100 elements is off (elementwise 0.5): numpy's linear interpolation
+    # puts the 99th percentile 1 % of the way from 0 to 0.5
+    assert r["p99"] == pytest.approx(0.005)
+    assert O.parity_report(ref2, ref2, out_bf16=False)["p99"] == 0.0
+
+
 def test_fp16_round_matches_torch():
     x = _rng(1).standard_normal(5000).astype(np.float32) * 100
     assert np.array_equal(O.fp16_round(x), torch.from_numpy(x).half().float().numpy())
@@ -124,7 +149,7 @@ def test_rms_norm_gated_bf16_chain_vs_torch_bf16():
     ref = (h * gv).to(torch.bfloat16).float().numpy()
     out = O.rms_norm_gated(x, gate, w, eps=1e-6, softcap=2.0, bf16=True, dtype=np.float32)
     # identical op order; libm vs torch transcendental ulps may flip a last bf16 bit
-    assert O.parity_err(out, ref, out_bf16=True) == 0.0
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= O.bf16_ulp(ref))
     assert np.mean(out == ref) > 0.99
 
 
