@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define MEMT_GDN2_ABI_VERSION 6
+#define MEMT_GDN2_ABI_VERSION 7
 
 #define MEMT_GDN2_OK 0
 #define MEMT_GDN2_EINVAL (-1)       /* null pointer or inconsistent sizes */
@@ -38,6 +38,10 @@ extern "C" {
 /* output gate of the readout epilogue */
 #define MEMT_GDN2_GATE_SOFTCAP_SILU 0 /* c * tanh(silu(g) / c): MemTRMSNormGated */
 #define MEMT_GDN2_GATE_SIGMOID 1      /* sigmoid(g) */
+
+/* memt_gdn2_readout_decode options */
+#define MEMT_GDN2_READOUT_L2NORM_Q 1   /* q rows are raw: q_hat = bf16(q / sqrt(sum q^2 + q_eps)) in the kernel */
+#define MEMT_GDN2_READOUT_STATE_BF16 2 /* the dot reads bf16(S), as the reference reader does */
 
 /* what the chunked update writes to `o` */
 #define MEMT_GDN2_OUT_NONE 0     /* state only */
@@ -271,6 +275,26 @@ int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void*
                             const void* gate, const void* weight, void* out, int B, int H, int K,
                             int V, float scale, float eps, float softcap, int gate_kind,
                             void* stream);
+
+/*
+ * The decode query path of the memory block in one kernel: for each query
+ * row b (one token per sample) and head h,
+ *   q_hat = l2norm(q[b,h])            (with MEMT_GDN2_READOUT_L2NORM_Q; else q is used as given)
+ *   r     = bf16(scale * q_hat^T S)   (S = state[slot(b),h]; bf16(S) with MEMT_GDN2_READOUT_STATE_BF16)
+ *   out   = MemTRMSNormGated(r, gate[b,h])   as memt_gdn2_readout_fused
+ * q [B, q_stride] bf16 rows holding H*K channels (a view of the fused QKV
+ * projection is read in place), gate [B, gate_stride] bf16 rows of H*V
+ * channels (strides in elements, at least the row width); S [slots, H, K, V] fp32,
+ * slot_idx [B] or NULL (slot = b).  Replaces the query path of
+ * QwenMemoryBlock.packed for length-1 samples (models/qwen/layer.py:112-131:
+ * l2norm -> memt_gdn2_read_fwd -> o_norm) and of the Flash block
+ * (models/deepseek/layer.py:174-183, snapshot_read with
+ * bf16_accumulator_output=True -> o_norm).
+ */
+int memt_gdn2_readout_decode(const float* S, const int32_t* slot_idx, const void* q, int64_t q_stride,
+                             const void* gate, int64_t gate_stride, const void* weight, void* out, int B,
+                             int H, int K, int V, float scale, float q_eps, float eps, float softcap,
+                             int gate_kind, int flags, void* stream);
 
 /*
  * Write gates of the memory block (models/qwen/layer.py:71-88; Flash:

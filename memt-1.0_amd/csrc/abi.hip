@@ -377,15 +377,41 @@ int memt_gdn2_rms_norm_gated(const void* x, const void* gate, const void* weight
 int memt_gdn2_readout_fused(const float* S, const int32_t* slot_idx, const void* q, const void* gate,
                             const void* weight, void* out, int B, int H, int K, int V, float scale, float eps,
                             float softcap, int gate_kind, void* stream) {
+  return memt_gdn2_readout_decode(S, slot_idx, q, (int64_t)H * K, gate, (int64_t)H * V, weight, out, B, H, K, V,
+                                  scale, 0.f, eps, softcap, gate_kind, 0, stream);
+}
+
+int memt_gdn2_readout_decode(const float* S, const int32_t* slot_idx, const void* q, int64_t q_stride,
+                             const void* gate, int64_t gate_stride, const void* weight, void* out, int B, int H,
+                             int K, int V, float scale, float q_eps, float eps, float softcap, int gate_kind,
+                             int flags, void* stream) {
   if (B < 0 || H <= 0) return MEMT_GDN2_EINVAL;
   if (!supported_kv(K, V)) return MEMT_GDN2_EUNSUPPORTED;
-  if (B > 0 && (S == nullptr || q == nullptr || gate == nullptr || weight == nullptr || out == nullptr))
-    return MEMT_GDN2_EINVAL;
+  if (flags & ~(MEMT_GDN2_READOUT_L2NORM_Q | MEMT_GDN2_READOUT_STATE_BF16)) return MEMT_GDN2_EINVAL;
+  if (B > 0) {
+    if (S == nullptr || q == nullptr || gate == nullptr || weight == nullptr || out == nullptr) return MEMT_GDN2_EINVAL;
+    if (q_stride < (int64_t)H * K || gate_stride < (int64_t)H * V) return MEMT_GDN2_EINVAL;
+  }
   if (!aligned16(S)) return MEMT_GDN2_EINVAL;
   if (gate_kind != MEMT_GDN2_GATE_SOFTCAP_SILU && gate_kind != MEMT_GDN2_GATE_SIGMOID) return MEMT_GDN2_EINVAL;
   if (gate_kind == MEMT_GDN2_GATE_SOFTCAP_SILU && !(softcap > 0.f)) return MEMT_GDN2_EINVAL;
-  return status_of(launch_readout(S, slot_idx, (const __bf16*)q, (const __bf16*)gate, (const __bf16*)weight,
-                                  (__bf16*)out, B, H, K, V, scale, eps, softcap, gate_kind, (hipStream_t)stream));
+  ReadoutArgs a{};
+  a.S = S;
+  a.slot_idx = slot_idx;
+  a.q = (const __bf16*)q;
+  a.gate = (const __bf16*)gate;
+  a.weight = (const __bf16*)weight;
+  a.out = (__bf16*)out;
+  a.q_stride = q_stride;
+  a.gate_stride = gate_stride;
+  a.H = H;
+  a.flags = flags;
+  a.scale = scale;
+  a.q_eps = q_eps;
+  a.eps = eps;
+  a.softcap = softcap;
+  a.gate_kind = gate_kind;
+  return status_of(launch_readout(a, B, K, V, (flags & MEMT_GDN2_READOUT_STATE_BF16) != 0, (hipStream_t)stream));
 }
 
 int memt_gdn2_write_gates(const void* decay, int64_t decay_stride, const void* decay_bias,

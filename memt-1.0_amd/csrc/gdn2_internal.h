@@ -54,6 +54,18 @@ __host__ __device__ __forceinline__ size_t align256(size_t x) { return (x + 255)
 //   decay f32  [K]       2^{gk_last}
 //   qg    f16  [64 x K]  P-frag, q * 2^{gk}                     (causal output)
 //   Aqk   f16  [64 x 64] P-frag, scale * causal scores          (causal output)
+//   uexp  i32  [NP]      U is stored as U * 2^-uexp per channel pass (see below)
+//
+// Value range.  W, kg, qg and Aqk are bounded by |q|, |k| <= 1 (l2-normalised
+// keys and queries), but U = A (beta v) and the state carry the values' own
+// magnitude, which may exceed the f16 range (65504).  The recurrence is linear
+// in (v, S) jointly and the columns of S are independent, so the value path
+// runs in powers of two: the WY stage stores U * 2^-uexp with uexp the
+// smallest e >= 0 with max|beta v| * 2^-e <= kValueRange (one exponent per
+// unit and channel pass), and every scan workgroup picks its own exponent for
+// its columns (its chunks' uexp and its starting state), rescales U by the
+// exact power of two and scales its outputs back on store.  With values below
+// kValueRange (the common case) every exponent is 0 and nothing is rescaled.
 struct WyBuffers {
   _Float16* W;
   _Float16* kgT;
@@ -61,10 +73,25 @@ struct WyBuffers {
   float* decay;
   _Float16* qg;
   _Float16* Aqk;
+  int32_t* uexp;
 };
 
+// Largest scaled |beta v| (and starting-state entry) the f16 value path
+// admits: the state then stays below ~sqrt(K) * 2 * kValueRange < 2^14 at d <= 512.
+constexpr float kValueRange = 256.f;
+
+// exponent e >= 0 with m * 2^-e <= kValueRange (m >= 0; 0 for m = 0)
+__device__ __forceinline__ int value_exponent(float m) {
+  int x = 0;
+  (void)frexpf(m, &x);  // m = f 2^x, f in [0.5, 1)
+  const int e = x - 8;  // kValueRange = 2^8
+  return e > 0 ? e : 0;
+}
+
+__host__ __device__ constexpr int wy_passes(int K) { return K > 256 ? K / 256 : 1; }
+
 struct WyLayout {
-  size_t off_W, off_kg, off_U, off_decay, off_qg, off_Aqk, total;
+  size_t off_W, off_kg, off_U, off_decay, off_qg, off_Aqk, off_uexp, total;
 };
 
 inline WyLayout wy_layout(int n_chunk, int H, int K, int V, bool causal) {
@@ -77,6 +104,7 @@ inline WyLayout wy_layout(int n_chunk, int H, int K, int V, bool causal) {
   l.off_decay = o; o = align256(o + units * K * 4);
   l.off_qg = o;    if (causal) o = align256(o + units * kChunk * K * 2);
   l.off_Aqk = o;   if (causal) o = align256(o + units * kChunk * kChunk * 2);
+  l.off_uexp = o;  o = align256(o + units * wy_passes(K) * 4);
   l.total = o;
   return l;
 }
@@ -90,6 +118,7 @@ inline WyBuffers wy_buffers(void* ws, const WyLayout& l, bool causal) {
   b.decay = (float*)(base + l.off_decay);
   b.qg = causal ? (_Float16*)(base + l.off_qg) : nullptr;
   b.Aqk = causal ? (_Float16*)(base + l.off_Aqk) : nullptr;
+  b.uexp = (int32_t*)(base + l.off_uexp);
   return b;
 }
 
@@ -221,6 +250,22 @@ struct PrologueArgs {
   float eps;
 };
 
+// Decode readout: one query row per sequence b; q and gate rows are
+// `q_stride` / `gate_stride` elements apart (head h at offset h*K / h*V).
+struct ReadoutArgs {
+  const float* S;           // [slots, H, K, V] fp32
+  const int32_t* slot_idx;  // [B] or null (slot = b)
+  const __bf16* q;          // [B, q_stride] l2-normalised, or raw with MEMT_GDN2_READOUT_L2NORM_Q
+  const __bf16* gate;       // [B, gate_stride]
+  const __bf16* weight;     // [V]
+  __bf16* out;              // [B, H*V]
+  int64_t q_stride, gate_stride;
+  int H;
+  int flags;                // MEMT_GDN2_READOUT_* bits
+  float scale, q_eps, eps, softcap;
+  int gate_kind;
+};
+
 // Launchers (return hipError_t of the launch).
 hipError_t launch_prologue(const PrologueArgs& a, int D, bool qk, hipStream_t stream);
 hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bool g_cumulative,
@@ -229,9 +274,7 @@ hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
                            int K, int V, float scale, hipStream_t stream, const int32_t* block_slot = nullptr);
-hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
-                          const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
-                          float eps, float softcap, int gate_kind, hipStream_t stream);
+hipError_t launch_readout(const ReadoutArgs& a, int B, int K, int V, bool state_bf16, hipStream_t stream);
 hipError_t launch_rms_norm_gated(const __bf16* x, const __bf16* gate, const __bf16* weight, __bf16* out,
                                  int64_t rows, int dim, float eps, float softcap, int gate_kind,
                                  hipStream_t stream);

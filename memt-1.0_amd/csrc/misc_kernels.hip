@@ -123,6 +123,12 @@ __device__ __forceinline__ __bf16 norm_gate_one(float x, float rs, float wt, flo
 // ---------------------------------------------------------------------------
 // Fused decode readout: one workgroup per (sequence, head).
 //   r = bf16(scale * q . S) (fp32 S, fp32 accumulation), then the epilogue.
+// Options (ReadoutArgs::flags):
+//   MEMT_GDN2_READOUT_L2NORM_Q  q is the raw projection row: the kernel forms
+//                               q_hat = bf16(q / sqrt(sum q^2 + q_eps)) first
+//                               (FLA l2norm_fwd, as the block's query path does);
+//   STATE_BF16 (template)       the dot reads bf16(S), the reference reader's
+//                               operand rounding (models/qwen/ops/_triton/read.py:64).
 // Thread (rg, cg) streams rows rg, rg + RG, rg + 2RG, ... of columns
 // [4cg, 4cg+4) with 16-byte loads, so one wave instruction reads 64 / CG
 // whole adjacent rows.  Every global load (q, gate, weight and the first NB
@@ -133,13 +139,8 @@ __device__ __forceinline__ __bf16 norm_gate_one(float x, float rs, float wt, flo
 // Threads of a readout workgroup: one per value column at d = 512.
 __host__ __device__ constexpr int readout_threads(int V) { return V > 256 ? V : 256; }
 
-template <int K, int V>
-__global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float* __restrict__ S, const int32_t* slot_idx,
-                                                      const __bf16* __restrict__ q,
-                                                      const __bf16* __restrict__ gate,
-                                                      const __bf16* __restrict__ weight,
-                                                      __bf16* __restrict__ out, int H, float scale,
-                                                      float eps, float softcap, int gate_kind) {
+template <int K, int V, bool STATE_BF16>
+__global__ __launch_bounds__(readout_threads(V)) void readout_kernel(ReadoutArgs a) {
   constexpr int NT = readout_threads(V);
   constexpr int CG = V / 4;          // float4 column groups
   constexpr int RG = NT / CG;        // row groups
@@ -149,22 +150,34 @@ __global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float
   __shared__ float q_s[NT];  // every thread stores: no branch before the first wait
   __shared__ float part[RG][V];
   __shared__ float red[NT / 64];
+  __shared__ float qred[NT / 64];
+  const int H = a.H;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int tid = threadIdx.x;
-  const int slot = slot_idx ? slot_idx[b] : b;
-  const float* Sp = S + ((size_t)slot * H + h) * K * V;
-  const size_t row = (size_t)b * H + h;
+  const int slot = a.slot_idx ? a.slot_idx[b] : b;
+  const float* Sp = a.S + ((size_t)slot * H + h) * K * V;
   const int cg = tid % CG, rg = tid / CG;
   // clamped indices keep these loads unconditional
-  const float qv = (float)q[row * K + (tid < K ? tid : K - 1)];
-  const float gv = (float)gate[row * V + (tid < V ? tid : V - 1)];
-  const float wv = (float)weight[tid < V ? tid : V - 1];
+  const float qv = (float)a.q[(size_t)b * a.q_stride + (size_t)h * K + (tid < K ? tid : K - 1)];
+  const float gv = (float)a.gate[(size_t)b * a.gate_stride + (size_t)h * V + (tid < V ? tid : V - 1)];
+  const float wv = (float)a.weight[tid < V ? tid : V - 1];
   asm volatile("" ::: "memory");  // issue q before the state rows: its wait then leaves them in flight
   f32x4 s4[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i)
     s4[i] = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)(i * RG + rg) * V + 4 * cg));
-  q_s[tid] = qv;
+  float qn = qv;
+  if (a.flags & MEMT_GDN2_READOUT_L2NORM_Q) {
+    // the query's l2 norm over its K channels (threads past K hold a clamped copy: excluded)
+    const float qsq = wave_sum(tid < K ? qv * qv : 0.f);
+    if ((tid & 63) == 0) qred[tid >> 6] = qsq;
+    lds_barrier();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < (K + 63) / 64; ++i) tot += qred[i];
+    qn = (float)(__bf16)(qv * (1.f / sqrtf(tot + a.q_eps)));
+  }
+  q_s[tid] = qn;
   lds_barrier();
   f32x4 acc = zero4();
 #pragma unroll
@@ -174,7 +187,7 @@ __global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float
       const int k = (j * NB + i) * RG + rg;
       const float qk = q_s[k];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = fmaf(qk, s4[i][e], acc[e]);
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(qk, STATE_BF16 ? (float)(__bf16)s4[i][e] : s4[i][e], acc[e]);
       if (j + 1 < RPT / NB)
         s4[i] = __builtin_nontemporal_load((const f32x4*)(Sp + (size_t)(k + NB * RG) * V + 4 * cg));
     }
@@ -187,7 +200,7 @@ __global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float
     float sum = 0.f;
 #pragma unroll
     for (int g2 = 0; g2 < RG; ++g2) sum += part[g2][tid];
-    r = (float)(__bf16)(sum * scale);  // the reader's bf16 output
+    r = (float)(__bf16)(sum * a.scale);  // the reader's bf16 output
     sq = r * r;
   }
   sq = wave_sum(sq);
@@ -197,8 +210,8 @@ __global__ __launch_bounds__(readout_threads(V)) void readout_kernel(const float
     float tot = 0.f;
 #pragma unroll
     for (int i = 0; i < (V + 63) / 64; ++i) tot += red[i];
-    const float rs = rsqrtf(tot / (float)V + eps);
-    out[row * V + tid] = norm_gate_one(r, rs, wv, gv, softcap, gate_kind);
+    const float rs = rsqrtf(tot / (float)V + a.eps);
+    a.out[((size_t)b * H + h) * V + tid] = norm_gate_one(r, rs, wv, gv, a.softcap, a.gate_kind);
   }
 }
 
@@ -301,9 +314,11 @@ __global__ __launch_bounds__(256) void wy_export_kernel(WyBuffers in, const int3
     if (kg) kg[dst] = (__bf16)(float)in.kgT[unit * C * K + pfrag_index(c, t, C)];
     if (qg && in.qg) qg[dst] = (__bf16)(float)in.qg[unit * C * K + pfrag_index(t, c, K)];
   }
+  constexpr int NP = wy_passes(K);
   for (int idx = threadIdx.x; idx < len * V; idx += 256) {
     const int t = idx / V, c = idx % V;
-    if (u) u[((size_t)(tok0 + t) * H + h) * V + c] = (__bf16)(float)in.U[unit * C * V + cfrag_index(t, c, V)];
+    const float us = ldexpf(1.f, in.uexp[unit * NP + c / (V / NP)]);  // U is stored as U * 2^-uexp
+    if (u) u[((size_t)(tok0 + t) * H + h) * V + c] = (__bf16)((float)in.U[unit * C * V + cfrag_index(t, c, V)] * us);
   }
   if (Aqk && in.Aqk) {
     for (int idx = threadIdx.x; idx < len * C; idx += 256) {
@@ -330,11 +345,28 @@ __global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const _
     out.W[unit * C * K + pfrag_index(t, c, K)] = (_Float16)(ok ? (float)w[src] : 0.f);
     out.kgT[unit * C * K + pfrag_index(c, t, C)] = (_Float16)(ok ? (float)kg[src] : 0.f);
   }
-  for (int idx = threadIdx.x; idx < C * V; idx += 256) {
-    const int t = idx / V, c = idx % V;
-    const bool ok = t < len;
-    out.U[unit * C * V + cfrag_index(t, c, V)] =
-        (_Float16)(ok ? (float)u[((size_t)(tok0 + t) * H + h) * V + c] : 0.f);
+  // U goes to f16 as U * 2^-uexp, uexp the value exponent of each channel pass's max |U|
+  constexpr int NP = wy_passes(K), VP = V / NP;
+  __shared__ float red[4];
+  for (int p = 0; p < NP; ++p) {
+    float m = 0.f;
+    for (int idx = threadIdx.x; idx < len * VP; idx += 256) {
+      const int t = idx / VP, c = p * VP + idx % VP;
+      m = fmaxf(m, fabsf((float)u[((size_t)(tok0 + t) * H + h) * V + c]));
+    }
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const int uexp = value_exponent(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    __syncthreads();  // red is reused by the next pass
+    const float us = ldexpf(1.f, -uexp);
+    if (threadIdx.x == 0) out.uexp[unit * NP + p] = uexp;
+    for (int idx = threadIdx.x; idx < C * VP; idx += 256) {
+      const int t = idx / VP, c = p * VP + idx % VP;
+      const bool ok = t < len;
+      out.U[unit * C * V + cfrag_index(t, c, V)] =
+          (_Float16)(ok ? (float)u[((size_t)(tok0 + t) * H + h) * V + c] * us : 0.f);
+    }
   }
   for (int c = threadIdx.x; c < K; c += 256)
     out.decay[unit * K + c] = fast_exp2(gk[((size_t)(tok0 + len - 1) * H + h) * K + c]);
@@ -363,16 +395,16 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_readout(const float* S, const int32_t* slot_idx, const __bf16* q, const __bf16* gate,
-                          const __bf16* weight, __bf16* out, int B, int H, int K, int V, float scale,
-                          float eps, float softcap, int gate_kind, hipStream_t stream) {
+hipError_t launch_readout(const ReadoutArgs& a, int B, int K, int V, bool state_bf16, hipStream_t stream) {
   if (B == 0) return hipSuccess;
-  dim3 grid(B * H);
-#define MEMT_RO(KK, VV)                                                                                   \
-  if (K == KK && V == VV) {                                                                               \
-    hipLaunchKernelGGL((readout_kernel<KK, VV>), grid, dim3(readout_threads(VV)), 0, stream, S, slot_idx, q, \
-                       gate, weight, out, H, scale, eps, softcap, gate_kind);                             \
-    return hipGetLastError();                                                                             \
+  dim3 grid(B * a.H);
+#define MEMT_RO(KK, VV)                                                                                      \
+  if (K == KK && V == VV) {                                                                                  \
+    if (state_bf16)                                                                                          \
+      hipLaunchKernelGGL((readout_kernel<KK, VV, true>), grid, dim3(readout_threads(VV)), 0, stream, a);     \
+    else                                                                                                     \
+      hipLaunchKernelGGL((readout_kernel<KK, VV, false>), grid, dim3(readout_threads(VV)), 0, stream, a);    \
+    return hipGetLastError();                                                                                \
   }
   MEMT_RO(64, 64)
   MEMT_RO(128, 128)

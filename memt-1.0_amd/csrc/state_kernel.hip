@@ -128,6 +128,10 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
+  // reduction steps whose f16(S) operands are read in one LDS batch (at most 16
+  // operands; one step at d = 512, whose registers are already full)
+  constexpr int SG = K > 256 ? 1 : KS * CT <= 16 ? KS : 16 / CT;
+  static_assert(KS % SG == 0, "operand batches");
   constexpr int SKP = K + kSPad;  // pitch of column-major f16(S)
   constexpr int VNP = C + kVPad;  // pitch of column-major f16(V_new)
   static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
@@ -192,6 +196,49 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   asm volatile("" ::: "memory");
 
+  // channel pass of this workgroup's value columns (d = 512: two passes of 256)
+  constexpr int NPU = wy_passes(K);
+  const int pu = NPU > 1 ? col0 / (V / NPU) : 0;
+  // Value exponent of this workgroup's columns: the largest of its chunks' U
+  // exponents and of its starting state's, so that U * 2^-ew and S * 2^-ew
+  // stay inside the f16 operand range.  The columns of S are independent, so
+  // every workgroup may use its own.  The transition (MODE 1) is scale-free.
+  int ew = 0;
+  if constexpr (MODE != 1) {
+    int eu = 0;
+    for (int c0 = c_begin; c0 < c_end; c0 += 64) {
+      const int c = c0 + lane;
+      if (c < c_end) eu = max(eu, a.in.uexp[((size_t)c * H + h) * NPU + pu]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) eu = max(eu, __shfl_xor(eu, off, 64));
+    float smax = 0.f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) smax = fmaxf(smax, fabsf(S[rt][ct][e]));
+    smax = wave_max(smax);
+    float* red = (float*)Vn_lds;  // free until the first chunk's V_new
+    if (lane == 0) red[w] = smax;
+    lds_barrier();
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < kScanThreads / 64; ++i) m = fmaxf(m, red[i]);
+    ew = __builtin_amdgcn_readfirstlane(max(eu, value_exponent(m)));
+    if (ew > 0) {
+      const float sc = ldexpf(1.f, -ew);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) S[rt][ct][e] *= sc;
+    }
+  }
+  const float oscale = ldexpf(1.f, ew);  // back to the values' own scale on store
+
   auto write_S_lds = [&]() {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -209,8 +256,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   // entry to a scalar register right after its load, waiting for every
   // outstanding prefetch; this way the wait comes once per 64 chunks.
   int mbase = c_begin - 64;
-  int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0;
-  int flags = 0, block = -1, tok0 = 0, len = 0;
+  int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0, m_eu = 0;
+  int flags = 0, block = -1, tok0 = 0, len = 0, eu_c = 0;
   auto meta = [&](int c) {
     if (c - mbase >= 64) {
       mbase = c;
@@ -222,6 +269,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         m_tok0 = ok ? a.chunk_tok0[cc] : 0;
         m_len = ok ? a.chunk_len[cc] : 0;
       }
+      if constexpr (MODE != 1) m_eu = ok ? a.in.uexp[((size_t)cc * H + h) * NPU + pu] : 0;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     const int i = c - mbase;
@@ -229,6 +277,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
     block = __builtin_amdgcn_readlane(m_block, i);
     tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
     len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
+    eu_c = MODE != 1 ? __builtin_amdgcn_readlane(m_eu, i) : 0;
   };
 
   F f;
@@ -312,11 +361,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int row = 16 * (q * RT + rt) + 4 * lg + e;
-                a.snaps[soff + (size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e];
+                a.snaps[soff + (size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e] * oscale;
               }
         }
       }
       const int cur_flags = flags, cur_tok0 = tok0, cur_len = len;
+      const float uscale = ldexpf(1.f, eu_c - ew);  // this chunk's U to the workgroup's scale (<= 1)
       meta(cn);
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
@@ -325,15 +375,27 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         acc[ct] = zero4();
         if constexpr (CAUSAL) acco[ct] = zero4();
       }
+      // The f16(S) operands of SG reduction steps are read from LDS in one
+      // batch ahead of their MFMAs (the scheduling barrier keeps the compiler
+      // from pairing each read with its own wait), so a batch costs one LDS
+      // latency instead of one per operand.
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
+      for (int s0 = 0; s0 < KS; s0 += SG) {
+        f16x8 sb[SG][CT];
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          const f16x8 sb = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s);
-          acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
-          if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
+        for (int s = 0; s < SG; ++s)
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) sb[s][ct] = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s0 + s);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < SG; ++s) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            acc[ct] = mfma_f16(f.w[s0 + s], sb[s][ct], acc[ct]);
+            if constexpr (CAUSAL) acco[ct] = mfma_f16(sb[s][ct], f.qg[s0 + s], acco[ct]);
+          }
+          load_w(cn, s0 + s);  // W and qg of the next chunk, step s0 + s
         }
-        load_w(cn, s);  // W and qg of the next chunk, step s
       }
       f16x4 un[CT];
 #pragma unroll
@@ -343,7 +405,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       for (int ct = 0; ct < CT; ++ct) {
         f16x4 vn;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)un[ct][e] - acc[ct][e]);
+        for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)un[ct][e] * uscale - acc[ct][e]);
         *(f16x4*)(&Vn_lds[(lcol0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
       }
       lds_barrier();
@@ -387,7 +449,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
           for (int ct = 0; ct < CT; ++ct) {
             bf16x4 o4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o4[e] = (__bf16)acco[ct][e];
+            for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(acco[ct][e] * oscale);
             *(bf16x4*)(orow + 16 * ct) = o4;
           }
         }
@@ -418,7 +480,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
-        *(f32x4*)(qo + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4) = S[rt][ct];
+        *(f32x4*)(qo + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4) = S[rt][ct] * oscale;
   } else if (last && a.ht != nullptr) {
     float* out = a.ht + ((size_t)(a.ht_slot ? a.ht_slot[seq] : seq) * H + h) * K * V;
 #pragma unroll
@@ -428,7 +490,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = 16 * (q * RT + rt) + 4 * lg + e;
-          out[(size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e];
+          out[(size_t)row * V + col0 + 16 * ct + lr] = S[rt][ct][e] * oscale;
         }
   }
 }

@@ -78,8 +78,8 @@ __device__ __forceinline__ void transpose_selectors(int lr, int lg, f16x8 (&sel)
     }
 }
 
-// Channel passes: d = 512 runs two passes of 256 channels through the same registers and LDS.
-__host__ __device__ constexpr int wy_passes(int K) { return K > 256 ? K / 256 : 1; }
+// Channel passes: d = 512 runs two passes of 256 channels through the same
+// registers and LDS (wy_passes in gdn2_internal.h).
 
 // RAW: the inputs are the memory block's projections (raw q, k, v, the decay
 // projection, erase and write logits); the kernel forms g, beta, q_hat and
@@ -115,6 +115,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   __shared__ __attribute__((aligned(16))) float Ld_s[4 * 16 * LQ];
   _Float16* const xw_s = xch_s;
   __shared__ float nrm_s[RAW && NCG > 1 ? 2 * NCG * C : 1];  // per-group l2norm sums
+  __shared__ float vmax_s[NT / 64];                           // per-wave max |beta v|
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
@@ -130,6 +131,8 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   const size_t rowV = ((size_t)(tok0 + (valid ? t : 0)) * H + h) * V;
 
   using BetaRaw = typename std::conditional<sizeof(BetaT) == 4, f32x4, bf16x4>::type;
+  // RAW: beta = bf16(sigmoid(write logit)), the reference's bf16 write gate
+  auto beta_of = [](float x) { return RAW ? (float)(__bf16)sigmoid_bf16(x) : x; };
   f32x4 Lt[4], Qt[4];  // L and Aqk tiles (I = wave, J <= I), summed over the passes
   if constexpr (NP > 1) {
 #pragma unroll
@@ -352,11 +355,34 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
         }
       }
     }
+    if constexpr (NP == 1) {
+      // the unit's max |beta v| (rows past the chunk end repeat row 0), for the
+      // value exponent of U; d > 256 forms it per pass in stage_x
+      float vmax = 0.f;
+#pragma unroll
+      for (int s = 0; s < VSL; ++s)
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            vmax = fmaxf(vmax, fabsf((float)vraw[s][half][e] * beta_of((float)btraw[s][half][e])));
+      vmax = wave_max(vmax);
+      if (lane == 0) vmax_s[tid >> 6] = vmax;
+    }
     lds_barrier();
 
+    float uscale = 1.f;  // 2^-uexp
+    if constexpr (NP == 1) {
+      float m = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < NT / 64; ++w2) m = fmaxf(m, vmax_s[w2]);
+      const int uexp = value_exponent(m);
+      uscale = ldexpf(1.f, -uexp);
+      if (tid == 0) a.out.uexp[unit] = uexp;
+    }
     f16x8 sel_h[2];
     transpose_selectors(lr, lg, sel_h);
-    // beta v to LDS, column-major (channel rows, token columns); read by the U product
+    // beta v * 2^-uexp to LDS, column-major (channel rows, token columns); read by the U product
 #pragma unroll
     for (int s = 0; s < (NP == 1 ? VSL : 0); ++s) {
       f16x8 xu8;
@@ -365,10 +391,8 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
 #pragma unroll
         for (int e = 0; e < 4; ++e)
         {
-          // RAW: beta = bf16(sigmoid(write logit)), the reference's bf16 write gate
-          const float bt = RAW ? (float)(__bf16)sigmoid_bf16((float)btraw[s][half][e])
-                               : (float)btraw[s][half][e];
-          xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * bt : 0.f);
+          const float bt = beta_of((float)btraw[s][half][e]);
+          xu8[4 * half + e] = (_Float16)(valid ? (float)vraw[s][half][e] * bt * uscale : 0.f);
         }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -718,25 +742,50 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     if constexpr (NP > 1) {
       const int vcb = p * VP + vcbl;
       const size_t tr = (size_t)(tok0 + (valid ? t : 0));
+      auto load_vb = [&](int s, int half, bf16x4& v4, BetaRaw& b4) {
+        const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
+        if constexpr (RAW) {  // projection rows; beta = bf16(sigmoid(write logit))
+          v4 = *(const bf16x4*)(a.v + tr * a.v_stride + h * V + c0);
+          b4 = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + h * V + c0);
+        } else {
+          v4 = *(const bf16x4*)(a.v + rowV + c0);
+          b4 = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+        }
+      };
+      // this pass's max |beta v| first (the rows are read again below, from
+      // the cache), then its value exponent
+      float vmax = 0.f;
+#pragma unroll
+      for (int s = 0; s < VSL; ++s)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          bf16x4 v4;
+          BetaRaw b4;
+          load_vb(s, half, v4, b4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vmax = fmaxf(vmax, fabsf((float)v4[e] * beta_of((float)b4[e])));
+        }
+      vmax = wave_max(vmax);
+      if (lane == 0) vmax_s[tid >> 6] = vmax;
+      lds_barrier();
+      float m = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < NT / 64; ++w2) m = fmaxf(m, vmax_s[w2]);
+      const int uexp = value_exponent(m);
+      const float us = ldexpf(1.f, -uexp);
+      if (tid == 0) a.out.uexp[unit * NP + p] = uexp;
 #pragma unroll
       for (int s = 0; s < VSL; ++s) {
         f16x8 xu8;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
           bf16x4 v4;
           BetaRaw b4;
-          if constexpr (RAW) {  // projection rows; beta = bf16(sigmoid(write logit))
-            v4 = *(const bf16x4*)(a.v + tr * a.v_stride + h * V + c0);
-            b4 = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + h * V + c0);
-          } else {
-            v4 = *(const bf16x4*)(a.v + rowV + c0);
-            b4 = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
-          }
+          load_vb(s, half, v4, b4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float bt = RAW ? (float)(__bf16)sigmoid_bf16((float)b4[e]) : (float)b4[e];
-            xu8[4 * half + e] = (_Float16)(valid ? (float)v4[e] * bt : 0.f);
+            const float bt = beta_of((float)b4[e]);
+            xu8[4 * half + e] = (_Float16)(valid ? (float)v4[e] * bt * us : 0.f);
           }
         }
 #pragma unroll

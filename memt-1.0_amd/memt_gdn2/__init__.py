@@ -23,6 +23,7 @@ from .ops import (
     l2norm_fwd,
     memt_gdn2_fwd_h,
     memt_gdn2_read_fwd,
+    readout_decode,
     readout_fused,
     rms_norm_gated,
     snapshot_read,
@@ -59,6 +60,7 @@ __all__ = [
     "memt_gdn2_fwd_h",
     "memt_gdn2_read_fwd",
     "readout_fused",
+    "readout_decode",
     "rms_norm_gated",
     "snapshot_read",
     "token_memory_packed",

@@ -26,6 +26,9 @@ BF16 = 1
 GATE_SOFTCAP_SILU = 0
 GATE_SIGMOID = 1
 
+READOUT_L2NORM_Q = 1
+READOUT_STATE_BF16 = 2
+
 OUT_NONE = 0
 OUT_SNAPSHOT = 1
 OUT_CAUSAL = 2
@@ -33,7 +36,7 @@ OUT_CAUSAL = 2
 CHUNK_BLOCK_START = 1
 CHUNK_COMMIT = 2
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class Plan(ctypes.Structure):
@@ -87,6 +90,8 @@ _SIGNATURES = {
     "memt_gdn2_read_fwd_slots": (_I, [_P, _P, _I, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _P]),
     "memt_gdn2_rms_norm_gated": (_I, [_P, _P, _P, _P, _I64, _I, _F, _F, _I, _P]),
     "memt_gdn2_readout_fused": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _F, _F, _I, _P]),
+    "memt_gdn2_readout_decode": (
+        _I, [_P, _P, _P, _I64, _P, _I64, _P, _P, _I, _I, _I, _I, _F, _F, _F, _F, _I, _I, _P]),
     "memt_gdn2_plan_count": (_I, [_P, _I, _I, _P]),
     "memt_gdn2_plan_build": (_I, [_P, _I, _P, _I, _P, _I, _P, _I, ctypes.c_int32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "memt_gdn2_write_gates": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I, _I, _P]),

@@ -6,7 +6,9 @@ and its ``packed`` entry (models/qwen/layer.py:99-152), the one call the
 serving runtime makes per memory layer.  The dense projections stay torch
 GEMMs (hipBLASLt).  Everything after them runs in this package's kernels:
 
-* query samples: ``l2norm`` -> ``memt_gdn2_read_fwd`` -> ``MemTRMSNormGated``;
+* decode batches (every query sample one token long): one fused kernel,
+  ``l2norm(q)``, the read of each sample's state and ``MemTRMSNormGated``;
+* other query samples: ``l2norm`` -> ``memt_gdn2_read_fwd`` -> ``MemTRMSNormGated``;
 * commit samples: the update with the gate and q/k prologue inside its WY
   kernel (``fused_prologue=True``, the default), or one prologue kernel
   (gates, ``l2norm(q)``, ``sqrt_b * l2norm(k)``) then ``token_memory_packed``;
@@ -29,9 +31,9 @@ from torch.nn import functional as F
 
 from .layout import WY_TILE_TOKENS, build_chunk_plan, validate_packed_inputs
 from .norm import MemTRMSNormGated
-from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, snapshot_read, token_memory_packed,
-                  token_memory_packed_flash, token_memory_packed_fused, token_memory_packed_fused_slots,
-                  token_memory_packed_slots)
+from .ops import (l2norm, memory_prologue, memt_gdn2_read_fwd, read_slots, readout_decode, snapshot_read,
+                  token_memory_packed, token_memory_packed_flash, token_memory_packed_fused,
+                  token_memory_packed_fused_slots, token_memory_packed_slots)
 
 
 class QwenMemoryBlock(nn.Module):
@@ -81,6 +83,9 @@ class QwenMemoryBlock(nn.Module):
         weight = self.in_proj.weight
         q, k, v = F.linear(hidden_batch, weight[: self.qkv_width]).split(self.qkv_rows, dim=-1)
         output_gate = self.g_down(F.linear(hidden_batch, weight[-D:]))
+        if not commit and _all_decode(lengths):
+            out = _decode_readout(self, q, output_gate, read_states, None)
+            return out.view(T, self.value_dim), None
         if not commit:
             # host boundaries: the plan is built without a device-to-host copy
             samples = [0, *accumulate(int(n) for n in lengths)]
@@ -125,6 +130,9 @@ class QwenMemoryBlock(nn.Module):
         weight = self.in_proj.weight
         q, k, v = F.linear(hidden_batch, weight[: self.qkv_width]).split(self.qkv_rows, dim=-1)
         output_gate = self.g_down(F.linear(hidden_batch, weight[-D:]))
+        if not commit and _all_decode(lengths):
+            out = _decode_readout(self, q, output_gate, pool.view(-1, H, D, D), read_slot)
+            return out.view(T, self.value_dim)
         if not commit:
             q_hat = l2norm(q.reshape(1, T, H, D))
             read = read_slots(q_hat, pool, read_slot, lengths, self.read_scale)
@@ -150,6 +158,25 @@ class QwenMemoryBlock(nn.Module):
         """Single-request entry (models/qwen/layer.py:154-161)."""
         return self.packed(hidden_states, initial_state, lengths=[len(hidden_states)], commit=commit,
                            write_states=initial_state)
+
+
+def _all_decode(lengths) -> bool:
+    """A query batch of one token per sample (the decode step)."""
+    return all(int(n) == 1 for n in lengths)
+
+
+def _decode_readout(block, q, output_gate, states, slots):
+    """Decode query path of either block in one kernel: ``l2norm(q)``, the
+    snapshot read ``bf16(scale * q_hat . bf16(S))`` of each sample's state and
+    ``o_norm`` with the output gate (the reference's l2norm -> reader ->
+    o_norm chain for length-1 samples, same roundings).  ``q`` and
+    ``output_gate`` are the projection rows ``[1, T, H*D]``; ``states``
+    ``[N, H, D, D]`` read at row ``n`` (or pool ``[slots, H, D, D]`` read at
+    ``slots[n]``)."""
+    norm = block.o_norm
+    return readout_decode(states, q, output_gate, norm.weight.to(torch.bfloat16), num_heads=block.num_heads,
+                          scale=block.read_scale, eps=norm.variance_epsilon, softcap=norm.output_gate_softcap_limit,
+                          gate_kind=norm.gate_kind, q_eps=1e-6, slot_idx=slots, state_bf16=True)
 
 
 def _latent_norm(inputs, weight, eps):
@@ -241,6 +268,8 @@ class DeepSeekMemoryBlock(nn.Module):
         validate_packed_inputs(self, hidden_states, read_states, write_states, lengths)
         T, H, D = len(hidden_states), self.num_heads, self.head_dim
         q, k, v, output_gate, erase, write, decay = self._project(hidden_states)
+        if not commit and _all_decode(lengths):
+            return _decode_readout(self, q, output_gate, read_states, None).view(T, self.value_dim), None
         if not commit:
             q_hat = l2norm(q.reshape(1, T, H, D))
             read = snapshot_read(q_hat, read_states, lengths, self.read_scale, bf16_accumulator_output=True)
@@ -269,6 +298,8 @@ class DeepSeekMemoryBlock(nn.Module):
         if pool.device != hidden_states.device or pool.dtype != torch.float32 or pool.shape[-3:] != (H, D, D):
             raise ValueError(f"Memory expects an FP32 state pool [slots, ..., {H}, {D}, {D}] on the hidden device")
         q, k, v, output_gate, erase, write, decay = self._project(hidden_states)
+        if not commit and _all_decode(lengths):
+            return _decode_readout(self, q, output_gate, pool.view(-1, H, D, D), read_slot).view(T, self.value_dim)
         if not commit:
             read = read_slots(l2norm(q.reshape(1, T, H, D)), pool, read_slot, lengths, self.read_scale)
             return self._output(read, output_gate)

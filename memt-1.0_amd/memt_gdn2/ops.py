@@ -29,6 +29,7 @@ __all__ = [
     "chunk_gdn2",
     "rms_norm_gated",
     "readout_fused",
+    "readout_decode",
     "workspace_bytes",
     "write_gates",
     "memory_prologue",
@@ -236,8 +237,15 @@ def memt_gdn2_read_fwd(q: torch.Tensor, snaps: torch.Tensor, plan: ChunkPlan, sc
 
 
 def snapshot_read(query, states, lengths, scale, *, bf16_accumulator_output: bool = False):
-    """Flash reader (models/deepseek/ops/read.py:6-31): each sample's tokens
-    read ``scale * q . bf16(S_sample)`` with fp32 accumulation, bf16 out."""
+    """Flash reader (models/deepseek/ops/read.py:6-31) with
+    ``bf16_accumulator_output=True``, the mode the Flash block uses: each
+    sample's tokens read ``bf16(scale * q . bf16(S_sample))`` (fp32
+    accumulation, one rounding).  The reference's ``False`` mode rounds the
+    dot to bf16 before scaling; that rounding is not implemented, so ``False``
+    raises rather than silently returning the one-rounding result."""
+    if not bf16_accumulator_output:
+        raise ValueError("snapshot_read implements bf16_accumulator_output=True only "
+                         "(bf16(scale * q . bf16(S)), one rounding)")
     samples = [0]
     for n in lengths:
         samples.append(samples[-1] + int(n))
@@ -409,6 +417,52 @@ def readout_fused(states, q, gate, weight, *, scale: float, eps: float, softcap:
                                     weight.data_ptr(), out.data_ptr(), B, H, K, V, float(scale), float(eps),
                                     float(softcap), _GATES[gate_kind], _lib.stream_of(q.device)),
         "readout_fused",
+    )
+    return out
+
+
+def readout_decode(states, q, gate, weight, *, num_heads: int, scale: float, eps: float, softcap: float = 2.0,
+                   gate_kind: str = "softcap_silu", q_eps: float = 1e-6, slot_idx=None, normalize_q: bool = True,
+                   state_bf16: bool = True):
+    """The memory block's decode query path in one kernel: one query token per
+    sample, ``q_hat = l2norm(q)``, ``r = bf16(scale * q_hat . S)`` and
+    ``MemTRMSNormGated(r, gate)`` (models/qwen/layer.py:112-131 for
+    length-1 samples; Flash: models/deepseek/layer.py:174-183).
+
+    ``q`` [..., B, H*K] raw bf16 projection rows (row views of the fused QKV
+    projection are read in place), ``gate`` [..., B, H*V] bf16 rows,
+    ``states`` [slots, H, K, V] fp32 read at ``slot_idx[b]`` (default ``b``).
+    ``state_bf16`` rounds S to bf16 inside the dot, as the reference reader
+    does.  Returns [B, H*V] bf16."""
+    lib = _lib.load()
+    _lib.require_gpu(states, q, gate, weight)
+    if gate_kind not in _GATES:
+        raise ValueError(f"gate_kind must be one of {sorted(_GATES)}")
+    H = num_heads
+    if states.ndim != 4 or states.shape[1] != H or states.dtype != torch.float32 or not states.is_contiguous():
+        raise ValueError(f"states must be contiguous fp32 [slots, {H}, K, V]")
+    K, V = states.shape[2], states.shape[3]
+    q2, qs = _rows(q, H * K, "q")
+    g2, gs = _rows(gate, H * V, "gate")
+    B = q2.shape[0]
+    if g2.shape[0] != B:
+        raise ValueError("q and gate must hold the same number of query rows")
+    if weight.shape != (V,) or weight.dtype != torch.bfloat16:
+        raise ValueError("weight must be bf16 [V]")
+    if slot_idx is None:
+        if states.shape[0] < B:
+            raise ValueError("fewer state slots than query rows")
+    else:
+        slot_idx = _slot_index(slot_idx, B, states.shape[0], q.device, "slot_idx")
+    flags = (_lib.READOUT_L2NORM_Q if normalize_q else 0) | (_lib.READOUT_STATE_BF16 if state_bf16 else 0)
+    (weight,) = _contig(weight)
+    out = torch.empty(B, H * V, dtype=torch.bfloat16, device=q.device)
+    _lib.check(
+        lib.memt_gdn2_readout_decode(states.data_ptr(), _lib.ptr(slot_idx), q2.data_ptr(), qs, g2.data_ptr(), gs,
+                                     weight.data_ptr(), out.data_ptr(), B, H, K, V, float(scale), float(q_eps),
+                                     float(eps), float(softcap), _GATES[gate_kind], flags,
+                                     _lib.stream_of(q.device)),
+        "readout_decode",
     )
     return out
 

@@ -106,3 +106,4 @@ def test_python_layer_fails_loudly_without_gpu():
 
     with pytest.raises(ValueError, match="GPU"):
         memt_gdn2.l2norm_fwd(torch.zeros(2, 64, dtype=torch.bfloat16))
+

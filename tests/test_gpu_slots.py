@@ -59,7 +59,7 @@ def test_read_slots_match_gather(dev):
     q = torch.nn.functional.normalize(torch.randn(1, T, H, D, device=dev), dim=-1).to(torch.bfloat16)
     pool = torch.randn(5, H, D, D, device=dev) * 0.1
     slots = [4, 1, 2]
-    ref = memt_gdn2.snapshot_read(q, pool[slots], lengths, D ** -0.5)
+    ref = memt_gdn2.snapshot_read(q, pool[slots], lengths, D ** -0.5, bf16_accumulator_output=True)
     out = memt_gdn2.read_slots(q, pool, slots, lengths, D ** -0.5)
     assert torch.equal(out, ref)
     with pytest.raises(ValueError):
