@@ -30,6 +30,10 @@ extern "C" {
 #define MEMT_GDN2_EUNSUPPORTED (-2) /* head dim / dtype without a compiled variant */
 #define MEMT_GDN2_ELAUNCH (-3)      /* the HIP launch reported an error */
 #define MEMT_GDN2_EWORKSPACE (-4)   /* workspace missing or too small */
+#define MEMT_GDN2_ESCRATCH (-5)     /* beyond the static scratch of memt_gdn2_chunk_update_noalloc */
+
+/* device scratch of memt_gdn2_chunk_update_noalloc, per GPU (64 MiB) */
+#define MEMT_GDN2_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* element types */
 #define MEMT_GDN2_F32 0
@@ -169,6 +173,26 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
                            float* ht, const float* read_states, float* snaps, void* o,
                            const memt_gdn2_plan* plan, int64_t T, int H, int K, int V, float scale,
                            int out_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * memt_gdn2_chunk_update without a workspace argument and without allocating:
+ * the workspace is the library's own static device scratch of
+ * MEMT_GDN2_NOALLOC_SCRATCH_BYTES per GPU (its address is looked up once per
+ * device, on the first call with that device current).  It has no counterpart
+ * in the reference; it serves callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Returns MEMT_GDN2_ESCRATCH when
+ * memt_gdn2_chunk_update_workspace_size(...) exceeds the scratch (about 900
+ * 64-token chunk-heads at d = 128 with the causal output).  Every call on one
+ * GPU uses the same scratch: calls that overlap on one GPU (concurrent
+ * streams) race and must be serialised by the caller.  Arguments and results
+ * are those of memt_gdn2_chunk_update.
+ */
+int memt_gdn2_chunk_update_noalloc(const void* q, const void* k, const void* v, const float* g,
+                                   const void* beta, int beta_dtype, const void* b, const float* h0,
+                                   float* ht, const float* read_states, float* snaps, void* o,
+                                   const memt_gdn2_plan* plan, int64_t T, int H, int K, int V,
+                                   float scale, int out_mode, void* stream);
 
 /*
  * memt_gdn2_chunk_update on a pool of state slots, in place: no gather of the

@@ -1,6 +1,8 @@
 // extern "C" entry points of libmemt_gdn2.so (declared in include/memt_gdn2.h).
 // Host-side argument checks, workspace carving and kernel dispatch.  No entry
 // point allocates memory or synchronises the host.
+#include <mutex>
+
 #include "gdn2_internal.h"
 
 using namespace memt;
@@ -69,6 +71,7 @@ const char* memt_gdn2_strerror(int status) {
     case MEMT_GDN2_EUNSUPPORTED: return "unsupported head dimension or dtype";
     case MEMT_GDN2_ELAUNCH: return "kernel launch failed";
     case MEMT_GDN2_EWORKSPACE: return "workspace missing or too small";
+    case MEMT_GDN2_ESCRATCH: return "problem needs more than the static scratch of the no-allocation entry point";
     default: return "unknown status";
   }
 }
@@ -225,6 +228,32 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   return status_of(launch_state(sa, K, V, causal, st));
 }
 
+// Static scratch of memt_gdn2_chunk_update_noalloc: the chunked update's
+// workspace for callers that cannot allocate.  One copy per GPU, held from the
+// module's load until the process ends; every call on a GPU reuses it (calls
+// that overlap on one GPU race on it).  Its contents need no clearing between
+// calls: every workspace byte a call reads was written earlier in that call.
+__device__ __align__(256) unsigned char scratch[MEMT_GDN2_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on each GPU (the host-side symbol is only a
+// stand-in), looked up once per device with that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MEMT_GDN2_ELAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return MEMT_GDN2_ELAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MEMT_GDN2_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -235,6 +264,20 @@ int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const fl
                            float scale, int out_mode, void* workspace, size_t workspace_bytes, void* stream) {
   return chunk_update(q, k, v, g, beta, beta_dtype, b, h0, ht, read_states, snaps, o, plan, T, H, K, V, scale,
                       out_mode, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int memt_gdn2_chunk_update_noalloc(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                   int beta_dtype, const void* b, const float* h0, float* ht,
+                                   const float* read_states, float* snaps, void* o, const memt_gdn2_plan* plan,
+                                   int64_t T, int H, int K, int V, float scale, int out_mode, void* stream) {
+  if (!plan_ok(plan) || H <= 0 || K <= 0 || V <= 0) return MEMT_GDN2_EINVAL;
+  const size_t need = memt_gdn2_chunk_update_workspace_size(plan->n_chunk, plan->n_seq, H, K, V, out_mode);
+  if (need > MEMT_GDN2_NOALLOC_SCRATCH_BYTES) return MEMT_GDN2_ESCRATCH;
+  void* ws = nullptr;
+  const int st = scratch_of_current_device(&ws);
+  if (st != MEMT_GDN2_OK) return st;
+  return chunk_update(q, k, v, g, beta, beta_dtype, b, h0, ht, read_states, snaps, o, plan, T, H, K, V, scale,
+                      out_mode, ws, MEMT_GDN2_NOALLOC_SCRATCH_BYTES, stream, nullptr, nullptr, nullptr);
 }
 
 int memt_gdn2_chunk_update_fused(const memt_gdn2_projections* x, void* q_hat, const float* h0, float* ht,

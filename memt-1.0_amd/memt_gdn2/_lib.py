@@ -19,6 +19,8 @@ EINVAL = -1
 EUNSUPPORTED = -2
 ELAUNCH = -3
 EWORKSPACE = -4
+ESCRATCH = -5
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 F32 = 0
 BF16 = 1
@@ -72,6 +74,10 @@ _SIGNATURES = {
     "memt_gdn2_chunk_update": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
+    "memt_gdn2_chunk_update_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _PLAN, _I64, _I, _I, _I, _F, _I, _P],
     ),
     "memt_gdn2_chunk_update_fused": (
         _I,

@@ -107,3 +107,23 @@ def test_python_layer_fails_loudly_without_gpu():
     with pytest.raises(ValueError, match="GPU"):
         memt_gdn2.l2norm_fwd(torch.zeros(2, 64, dtype=torch.bfloat16))
 
+
+def test_noalloc_rejects_problems_beyond_its_scratch(lib):
+    """The no-allocation update checks its static scratch before touching the
+    device: a plan needing more returns MEMT_GDN2_ESCRATCH (and the size
+    function agrees with the scratch limit the header states)."""
+    assert b"static scratch" in lib.memt_gdn2_strerror(_lib.ESCRATCH)
+    dummy = (ctypes.c_int32 * 1)()
+    n_chunk = 4096  # 4096 chunks x 16 heads at d=128: ~290 MiB of workspace
+    plan = _lib.Plan(chunk_tok0=ctypes.addressof(dummy), chunk_len=ctypes.addressof(dummy),
+                     seq_chunk_offsets=ctypes.addressof(dummy), chunk_block_ids=None, chunk_flags=None,
+                     n_chunk=n_chunk, n_seq=1, n_block=1, reserved=0)
+    need = lib.memt_gdn2_chunk_update_workspace_size(n_chunk, 1, 16, 128, 128, _lib.OUT_CAUSAL)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    st = lib.memt_gdn2_chunk_update_noalloc(None, None, None, None, None, _lib.F32, None, None, None, None, None,
+                                            None, ctypes.byref(plan), 64 * n_chunk, 16, 128, 128, 0.088,
+                                            _lib.OUT_CAUSAL, None)
+    assert st == _lib.ESCRATCH
+    assert lib.memt_gdn2_chunk_update_noalloc(None, None, None, None, None, _lib.F32, None, None, None, None, None,
+                                              None, None, 0, 16, 128, 128, 0.088, _lib.OUT_CAUSAL,
+                                              None) == _lib.EINVAL
