@@ -229,14 +229,14 @@ def bench_prologue(dev, reps=20, T=8192, H=16, D=128):
     }
 
 
-def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32):
+def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32, cpu=True):
     """The wide-state Flash-like shape: chunked update (causal) and a batch-B readout."""
     steps = min(steps, 20)
     up = bench_update(dev, steps, warmup, T, H, D, out_mode="causal", on_device=True)
     ro = bench_readout(dev, steps, warmup, B=B, H=H, D=D)
     ub, uf = update_bytes(T, H, D, D), update_flops(T, H, D, D, causal=True)
     t = up["event_ms_mean"] * 1e-3
-    return {
+    res = {
         "metric": "wide-state GDN-2 update tokens/s @H64 d256 T16K; decode readout GB/s @B32",
         "value": T / (up["ms_per_step"] * 1e-3), "unit": "tokens/s", "steps": steps, "warmup": warmup,
         "ms_per_step": up["ms_per_step"], "dtype": "bf16", "data": "synthetic (same distributions, drawn on the GPU)",
@@ -247,9 +247,12 @@ def bench_wide(dev, steps, warmup, T=16384, H=64, D=256, B=32):
         "readout": {"workload": f"decode readout B={B} H={H} dk=dv={D}", "value": ro["gbs"], "unit": "GB/s",
                     "us_per_launch": ro["ms_per_launch"] * 1e3, "frac": ro["gbs"] / HBM_PEAK_GBS},
     }
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline_chunked(T, H, D, heads=4)
+    return res
 
 
-def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8):
+def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8, cpu=True):
     """The Flash model's memory shape (d=512, models/deepseek/ops/packed.py:70-108):
     a commit in snapshot mode (every token reads the incoming state, final
     state out) and a batch-B decode readout."""
@@ -258,7 +261,7 @@ def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8):
     ro = bench_readout(dev, steps, warmup, B=B, H=H, D=D)
     ub, uf = update_bytes(T, H, D, D), update_flops(T, H, D, D, causal=False) + 2 * T * H * D * D
     t = up["event_ms_mean"] * 1e-3
-    return {
+    res = {
         "metric": "Flash-shape GDN-2 commit tokens/s @H64 d512 T8K; decode readout GB/s @B8",
         "value": T / (up["ms_per_step"] * 1e-3), "unit": "tokens/s", "steps": steps, "warmup": warmup,
         "ms_per_step": up["ms_per_step"], "dtype": "bf16", "data": "synthetic (same distributions, drawn on the GPU)",
@@ -269,6 +272,199 @@ def bench_flash(dev, steps, warmup, T=8192, H=64, D=512, B=8):
         "readout": {"workload": f"decode readout B={B} H={H} dk=dv={D}", "value": ro["gbs"], "unit": "GB/s",
                     "us_per_launch": ro["ms_per_launch"] * 1e3, "frac": ro["gbs"] / HBM_PEAK_GBS},
     }
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline_chunked(T, H, D, heads=2, out_mode="snapshot")
+    return res
+
+
+def segment_lengths(total=65536, n=4, seed=20261204):
+    """The varlen workload's segment lengths: n draws from U[1024, 32768],
+    rescaled to sum to `total` (rounded, the last one absorbing the rest)."""
+    rng = np.random.default_rng(seed)
+    raw = rng.uniform(1024, 32768, n)
+    lengths = [int(round(x)) for x in raw * total / raw.sum()]
+    lengths[-1] = total - sum(lengths[:-1])
+    return lengths
+
+
+def cpu_baseline_chunked(T, H, D, *, heads, runs=3, out_mode="causal", segments=None):
+    """The PyTorch-CPU chunked port (oracle/gdn2_torch.py) on `heads` of the H
+    heads (all T tokens), fp32, median of `runs`; the rate is scaled to all H
+    heads (heads are independent and the port's cost is linear in them)."""
+    from oracle.gdn2_torch import chunked_gdn2_torch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(20261207)
+    q = torch.nn.functional.normalize(torch.randn(T, heads, D, generator=g), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(T, heads, D, generator=g), dim=-1)
+    v = torch.randn(T, heads, D, generator=g)
+    lg = torch.nn.functional.logsigmoid(torch.randn(T, heads, D, generator=g))
+    beta = torch.sigmoid(torch.randn(T, heads, D, generator=g))
+    bounds = [0, T] if segments is None else [0, *np.cumsum(segments).tolist()]
+    h0 = torch.randn(len(bounds) - 1, heads, D, D, generator=g) * 0.02
+    chunked_gdn2_torch(q[:256], k[:256], v[:256], lg[:256], beta[:256], h0=h0[0], out_mode=out_mode)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for n in range(len(bounds) - 1):
+            a, b = bounds[n], bounds[n + 1]
+            chunked_gdn2_torch(q[a:b], k[a:b], v[a:b], lg[a:b], beta[a:b], h0=h0[n], out_mode=out_mode)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times) * H / heads
+    return dict(value=T / t, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{heads} of the {H} heads over all {T} tokens (d={D}, {out_mode}), fp32 torch CPU, median of "
+                       f"{runs} runs, scaled to {H} heads ({statistics.median(times):.2f} s per run)")
+
+
+def bench_varlen(dev, steps, warmup, T=65536, H=16, D=128, cpu=True):
+    """The varlen packed update: 4 segments (seeded lengths from U[1024, 32768]
+    rescaled to 65536 tokens), per-segment initial states, causal output and
+    per-segment final states."""
+    import memt_gdn2
+
+    lengths = segment_lengths(T)
+    cu = [0, *np.cumsum(lengths).tolist()]
+    N = len(lengths)
+    sets = []
+    for i in range(2):  # 2 x 1.9 GB of inputs: beyond the MALL
+        s = _inputs_on_device(T, H, D, D, seed=20261204 + i, dev=dev)
+        gen = torch.Generator(device=dev).manual_seed(20261214 + i)
+        s["h0"] = torch.randn(N, H, D, D, generator=gen, device=dev) * 0.02
+        sets.append(s)
+
+    def step(i):
+        s = sets[i % len(sets)]
+        return memt_gdn2.chunk_gdn2(s["q"], s["k"], s["v"], s["g"], s["beta"], initial_state=s["h0"],
+                                    cu_seqlens=cu, out_mode="causal")
+
+    steps = min(steps, 30)
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1) / steps
+    ub, uf = update_bytes(T, H, D, D, N=N), update_flops(T, H, D, D, causal=True)
+    out = {
+        "metric": "varlen GDN-2 update tokens/s @4 segments, 65536 tokens, H16 d128",
+        "value": T / (wall / steps), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": wall * 1e3 / steps, "dtype": "bf16", "data": "synthetic (same distributions, drawn on the GPU)",
+        "config": {"workload": f"varlen packed chunked GDN-2 update, segments {lengths} (cu_seqlens), H={H} "
+                               f"dk=dv={D} chunk=64, per-segment initial states, causal output + final states"},
+        "roofline": {"bound": "hbm", "achieved": ub / (ev_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ub / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": ub,
+                     "event_ms_per_launch": ev_ms, "mfma_frac": uf / (ev_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                     "algorithmic_flops": uf},
+    }
+    if cpu:
+        out["cpu_baseline"] = cpu_baseline_chunked(T, H, D, heads=4, segments=lengths)
+    return out
+
+
+def bench_cfg0(dev, reps=200, T=512, H=4, D=64, cpu=True):
+    """The naive-recurrence configuration (B=1 H=4 T=512 d=64, zero initial
+    state): the GPU update per call, and the reference's CPU path, the
+    token-by-token fp32 recurrence in torch (oracle/gdn2_torch.py)."""
+    import memt_gdn2
+    from oracle.gdn2_torch import recurrent_gdn2_torch
+
+    s = _inputs(T, H, D, D, seed=20261201, dev=dev)
+    h0 = torch.zeros(1, H, D, D, device=dev)
+    ms = _event_ms(lambda: memt_gdn2.chunk_gdn2(s["q"], s["k"], s["v"], s["g"], s["beta"], initial_state=h0,
+                                               out_mode="causal"), reps, warmup=10)
+    out = {"workload": f"naive-recurrence configuration B=1 H={H} T={T} dk=dv={D}, zero initial state, causal "
+                       f"output + final state",
+           "gpu_us_per_call": ms * 1e3, "gpu_tokens_per_s": T / (ms * 1e-3)}
+    if cpu:
+        torch.set_num_threads(os.cpu_count() or 1)
+        cpu_in = {n: s[n][0].float().cpu() for n in ("q", "k", "v", "g", "beta")}
+        recurrent_gdn2_torch(*(cpu_in[n][:16] for n in ("q", "k", "v", "g", "beta")))
+        times = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            recurrent_gdn2_torch(*(cpu_in[n] for n in ("q", "k", "v", "g", "beta")))
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        out["cpu_baseline"] = dict(value=T / t, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                                   sample=f"the whole configuration, token loop in fp32 torch CPU, median of 5 runs "
+                                          f"({t * 1e3:.1f} ms each)")
+    return out
+
+
+def bench_block_decode(dev, reps=50, B=64, H=16, D=128, hidden=2048):
+    """The memory block's decode step (QwenMemoryBlock.packed, commit=False,
+    B one-token samples): the q and output-gate projections (torch GEMMs)
+    plus the fused readout kernel, on rotating read-state sets (beyond the
+    MALL); and the fused readout kernel alone on the same sets."""
+    import types
+
+    import memt_gdn2
+    from memt_gdn2.block import QwenMemoryBlock
+
+    cfg = types.SimpleNamespace(hidden_size=hidden, num_heads=H, head_dim=D, chunk_tokens=2048, rms_norm_eps=1e-6,
+                                output_gate_softcap=2.0)
+    torch.manual_seed(20261208)
+    block = QwenMemoryBlock(cfg, device=dev)
+    with torch.no_grad():
+        for name, p in block.named_parameters():
+            p.copy_(torch.randn_like(p, dtype=torch.float32) * (p.shape[-1] ** -0.5 if p.ndim == 2 else 0.1))
+    nb = readout_bytes(B, H, D, D)
+    nsets = max(4, int(np.ceil(1.5 * MALL_BYTES / nb)))
+    g = torch.Generator(device=dev).manual_seed(20261209)
+    states = [torch.randn(B, H, D, D, generator=g, device=dev) * 0.02 for _ in range(nsets)]
+    xs = [torch.randn(B, hidden, generator=g, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    lengths = [1] * B
+    i = [0]
+
+    def step():
+        j = i[0] % nsets
+        i[0] += 1
+        return block.packed(xs[j], states[j], lengths=lengths, commit=False, write_states=states[j])
+
+    step_ms = _event_ms(step, reps, warmup=5)  # eager, host launch overhead included
+
+    def graph_ms(fn, passes, reps_):
+        """ms per call of fn() inside a captured graph of `passes` rounds over the sets."""
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(passes):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        return _event_ms(graph.replay, reps_, warmup=2) / (passes * nsets)
+
+    def steps_all():
+        for j in range(nsets):
+            block.packed(xs[j], states[j], lengths=lengths, commit=False, write_states=states[j])
+
+    step_graph_ms = graph_ms(steps_all, 2, 10)
+    W = H * D
+    qkvs = [torch.nn.functional.linear(x, block.in_proj.weight[:3 * W]) for x in xs]
+    gates = [torch.randn(B, W, generator=g, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    wn = block.o_norm.weight.to(torch.bfloat16)
+
+    def kernels_all():
+        for j in range(nsets):
+            memt_gdn2.readout_decode(states[j], qkvs[j][:, :W], gates[j], wn, num_heads=H, scale=D ** -0.5, eps=1e-6)
+
+    k_ms = graph_ms(kernels_all, 8, 20)
+    return {"workload": f"memory block decode step, QwenMemoryBlock.packed(commit=False), B={B} one-token samples, "
+                        f"H={H} d={D}, hidden {hidden}, {nsets} rotating read-state sets",
+            "ms_per_step": step_ms, "ms_per_step_graph": step_graph_ms,
+            "readout_kernel_us": k_ms * 1e3, "readout_kernel_gbs": nb / (k_ms * 1e-3) / 1e9,
+            "readout_kernel_hbm_frac": nb / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "note": "ms_per_step is eager (host launch overhead included); ms_per_step_graph and the kernel time "
+                    "come from captured graphs over the rotating sets"}
 
 
 def _roofs_lib():
@@ -309,9 +505,10 @@ def measured_roofs(dev, reps=20):
     read_ms = _event_ms(read, reps, warmup=3)
     del x
     iters = 2048
+    acc = torch.empty(blocks * 256 * MFMA_PROBE_CHAINS * 4, dtype=torch.float32, device=dev)
 
     def mfma():
-        if lib.memt_roofs_mfma(part.data_ptr(), blocks, iters, stream) != 0:
+        if lib.memt_roofs_mfma(acc.data_ptr(), blocks, iters, stream) != 0:
             raise RuntimeError("MFMA probe launch failed")
 
     mfma_ms = _event_ms(mfma, reps, warmup=3)
@@ -320,24 +517,26 @@ def measured_roofs(dev, reps=20):
     b = torch.randn(n, n, device=dev).to(torch.bfloat16)
     c = torch.empty(n, n, device=dev, dtype=torch.bfloat16)
     gemm_ms = _event_ms(lambda: torch.mm(a, b, out=c), reps, warmup=3)
-    del a, b, c, part
+    del a, b, c, part, acc
     torch.cuda.empty_cache()
     copy_gbs = 2 * COPY_BYTES / (copy_ms * 1e-3) / 1e9
     read_gbs = COPY_BYTES / (read_ms * 1e-3) / 1e9
     mfma_tflops = blocks * 4 * MFMA_PROBE_CHAINS * iters * MFMA_PROBE_FLOP / (mfma_ms * 1e-3) / 1e12
     gemm_tflops = 2 * n ** 3 / (gemm_ms * 1e-3) / 1e12
     return {
-        "hbm_read_gbs": read_gbs,
-        "hbm_read_frac_of_spec": read_gbs / HBM_PEAK_GBS,
-        "hbm_read_workload": f"streaming read of {COPY_BYTES >> 30} GiB (16-byte non-temporal loads, "
-                             f"{blocks} x 256 threads), mean of {reps}",
+        # a measured reference, not a roof: the decode readout, which issues its
+        # whole state read at once, streams faster than this probe
+        "streaming_read_probe_gbs": read_gbs,
+        "streaming_read_probe_frac_of_spec": read_gbs / HBM_PEAK_GBS,
+        "streaming_read_probe_workload": f"streaming read of {COPY_BYTES >> 30} GiB (16-byte non-temporal "
+                                         f"loads, {blocks} x 256 threads), mean of {reps}",
         "hbm_copy_gbs": copy_gbs,
         "hbm_copy_frac_of_spec": copy_gbs / HBM_PEAK_GBS,
         "hbm_copy_workload": f"torch device copy of {COPY_BYTES >> 30} GiB fp32 (read + write), mean of {reps}",
         "mfma_bf16_tflops": mfma_tflops,
         "mfma_bf16_frac_of_spec": mfma_tflops / MFMA_BF16_PEAK_TFLOPS,
         "mfma_bf16_workload": f"v_mfma_f32_16x16x32_bf16 loop, {MFMA_PROBE_CHAINS} chains x {iters} per wave, "
-                              f"{blocks * 4} waves, mean of {reps}",
+                              f"{blocks * 4} waves, every accumulator stored, mean of {reps}",
         "gemm_bf16_tflops": gemm_tflops,
         "gemm_bf16_frac_of_spec": gemm_tflops / MFMA_BF16_PEAK_TFLOPS,
         "gemm_bf16_workload": f"torch.mm bf16 {n}x{n}x{n} (hipBLASLt), mean of {reps}",
@@ -429,6 +628,10 @@ def main():
                     help="measure the wide-state workload instead (B=1 H=64 T=16384 d=256; batch-32 readout)")
     ap.add_argument("--flash", action="store_true",
                     help="measure the Flash memory shape instead (B=1 H=64 T=8192 d=512 commit; batch-8 readout)")
+    ap.add_argument("--varlen", action="store_true",
+                    help="measure the varlen packed update instead (4 segments, 65536 tokens, H=16 d=128)")
+    ap.add_argument("--probes", action="store_true",
+                    help="run only the measured roofs (read and MFMA probes, copy, GEMM), for counter runs")
     ap.add_argument("--calibrate", action="store_true",
                     help="run the hardware-counter workload (copy of known size, then update steps and readouts)")
     args = ap.parse_args()
@@ -448,11 +651,17 @@ def main():
     if args.calibrate:
         calibrate(dev, T, H, D)
         return
+    if args.probes:
+        print(json.dumps(measured_roofs(dev, reps=5)))
+        return
     if args.wide:
-        print(json.dumps(bench_wide(dev, args.steps, args.warmup)))
+        print(json.dumps(bench_wide(dev, args.steps, args.warmup, cpu=not args.no_cpu)))
         return
     if args.flash:
-        print(json.dumps(bench_flash(dev, args.steps, args.warmup)))
+        print(json.dumps(bench_flash(dev, args.steps, args.warmup, cpu=not args.no_cpu)))
+        return
+    if args.varlen:
+        print(json.dumps(bench_varlen(dev, args.steps, args.warmup, cpu=not args.no_cpu)))
         return
 
     roofs = measured_roofs(dev, reps=50)  # first: its 0.2 s of probes and GEMMs also brings the clocks up
@@ -461,6 +670,8 @@ def main():
             if args.mode == "causal" else None)
     ro = bench_readout(dev, args.steps, args.warmup)
     pro = bench_prologue(dev)
+    dec = bench_block_decode(dev)
+    cfg0 = bench_cfg0(dev, cpu=not args.no_cpu)
 
     causal = args.mode == "causal"
     up_traffic, ro_traffic = profiled_traffic()
@@ -517,10 +728,10 @@ def main():
         },
     }
     result["memory_block_commit"] = pro
+    result["memory_block_decode"] = dec
+    result["naive_recurrence_config"] = cfg0
     result["measured_roofs"] = roofs
-    result["roofline"]["frac_of_measured_read"] = achieved / roofs["hbm_read_gbs"]
     result["roofline"]["mfma_frac_of_measured"] = uf / t_up / 1e12 / roofs["mfma_bf16_tflops"]
-    result["readout"]["roofline"]["frac_of_measured_read"] = ro["gbs"] / roofs["hbm_read_gbs"]
     if snap is not None:
         result["snapshot_mode"] = {
             "workload": "token_memory_packed semantics (tokens read the incoming state), same shapes",

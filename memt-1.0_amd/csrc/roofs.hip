@@ -50,10 +50,10 @@ __global__ __launch_bounds__(kThreads) void mfma_probe(int iters, float* __restr
 #pragma unroll
     for (int j = 0; j < kChains; ++j) c[j] = memt::mfma_bf16(a, b, c[j]);
   }
-  float s = 0.f;
+  // every accumulator is stored, so no chain can be dropped as dead code
+  memt::f32x4* o = (memt::f32x4*)out + ((size_t)blockIdx.x * kThreads + threadIdx.x) * kChains;
 #pragma unroll
-  for (int j = 0; j < kChains; ++j) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
-  out[(size_t)blockIdx.x * kThreads + threadIdx.x] = s;
+  for (int j = 0; j < kChains; ++j) o[j] = c[j];
 }
 
 }  // namespace
@@ -67,7 +67,8 @@ int memt_roofs_read(const void* x, size_t bytes, float* out, int blocks, hipStre
   return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
-// blocks * 4 waves each run kChains * iters MFMAs of 16384 flop; out holds blocks * 256 floats.
+// blocks * 4 waves each run kChains * iters MFMAs of 16384 flop; out holds
+// blocks * 256 * kChains * 4 floats (every accumulator of every lane).
 int memt_roofs_mfma(float* out, int blocks, int iters, hipStream_t stream) {
   if (out == nullptr || blocks <= 0 || iters <= 0) return -1;
   hipLaunchKernelGGL(mfma_probe, dim3(blocks), dim3(kThreads), 0, stream, iters, out);

@@ -98,3 +98,23 @@ def readout_torch(S, q, gate, weight, *, scale, eps, softcap=2.0, gate_kind="sof
     else:
         s = softcap * torch.tanh(torch.nn.functional.silu(gz) / softcap)
     return (h * s).to(torch.bfloat16)
+
+
+def recurrent_gdn2_torch(q, k, v, g, beta, *, h0=None, scale=None, dtype=torch.float32):
+    """The naive token-by-token recurrence (TR Sec. 4.2, App. C eq. 22) in
+    torch on the CPU, one sequence: ``q,k,g [T,H,K]``, ``v,beta [T,H,V]``,
+    ``h0 [H,K,V]`` -> ``(o [T,H,V], ht [H,K,V])`` with the causal read
+    ``o_t = scale q_t^T S_t``.  The reference's CPU path for the
+    naive-recurrence configuration, timed as the CPU baseline."""
+    q, k, v, g, beta = (x.to(dtype) for x in (q, k, v, g, beta))
+    T, H, K = k.shape
+    V = v.shape[-1]
+    scale = K ** -0.5 if scale is None else scale
+    S = torch.zeros(H, K, V, dtype=dtype) if h0 is None else h0.to(dtype).clone()
+    o = torch.empty(T, H, V, dtype=dtype)
+    for t in range(T):
+        S = S * torch.exp(g[t]).unsqueeze(-1)
+        e = beta[t] * v[t] - torch.einsum("hk,hkv->hv", k[t], S)
+        S = S + k[t].unsqueeze(-1) * e.unsqueeze(1)
+        o[t] = scale * torch.einsum("hk,hkv->hv", q[t], S)
+    return o, S

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import gdn2 as O
-from gpu_util import bf, host, to_dev
+from gpu_util import bf, check, host, to_dev
 
 import memt_gdn2
 from memt_gdn2.runtime import MemoryRequest, MemoryRuntime, plan_of
@@ -104,3 +104,34 @@ def test_runtime_slot_io_matches_gather_path(dev):
     assert torch.equal(results[0][0], results[1][0])
     assert torch.equal(results[0][1], results[1][1])
     assert not torch.equal(results[1][1][4], storage0[4])  # the commit did write its slot
+
+
+@pytest.mark.parametrize("lengths,in_place", [([130, 1, 129], True), ([130, 1, 129], False), ([2100, 1900], True)])
+def test_slot_paths_against_the_oracle(dev, lengths, in_place):
+    """The slot-indexed update and reader pinned directly against the fp64
+    oracle's packed commit (models/qwen/ops/packed.py:34-81) on the same slot
+    contents: reads from pool[read_slots], scans from pool[write_slots], final
+    states into pool[write_slots] (in place when they are the read slots too)."""
+    print(f"slot paths vs oracle lengths={lengths} in_place={in_place}", flush=True)
+    H, D, N = 2, 128, len(lengths)
+    T = sum(lengths)
+    inp = O.synth_inputs(T, H, D, D, seed=800 + T)
+    beta = O.bf16_round(inp["beta"])
+    q, k, v, g = bf(inp["q"], dev), bf(inp["k"], dev), bf(inp["v"], dev), to_dev(inp["g"], dev)
+    pool_h = (np.random.default_rng(801).standard_normal((6, H, D, D)) * 0.05).astype(np.float32)
+    pool = to_dev(pool_h, dev)
+    write_slots = [4, 0, 2][:N]
+    read_slots = write_slots if in_place else [1, 5, 3][:N]
+    read = memt_gdn2.token_memory_packed_slots(q, k, v, g, bf(beta, dev), pool, read_slots, write_slots, erase=None,
+                                               lengths=lengths, scale=D ** -0.5, chunk_tokens=2048)
+    r_ref, f_ref = O.token_memory_packed(inp["q"], inp["k"], inp["v"], inp["g"], beta, pool_h[read_slots],
+                                         pool_h[write_slots], erase=None, lengths=lengths, scale=D ** -0.5,
+                                         chunk_tokens=2048)
+    check("slot commit read", host(read), r_ref, out_bf16=True)
+    check("slot commit final states", host(pool)[write_slots], f_ref, out_bf16=False)
+    untouched = [s for s in range(6) if s not in write_slots]
+    assert np.array_equal(host(pool)[untouched], pool_h[untouched])
+    # the query reader on the updated pool against the oracle's reader
+    qr = memt_gdn2.read_slots(q, pool, read_slots, lengths, D ** -0.5)
+    check("slot query read", host(qr), O.snapshot_read(inp["q"], host(pool)[read_slots], lengths, D ** -0.5),
+          out_bf16=True)

@@ -440,3 +440,17 @@ def test_planted_mistakes_are_caught(kind):
     # every planted mistake must fail at least one pin (the read-back invariant is
     # decay-agnostic by design, so a wrong decay base is caught by the product form)
     assert any(caught), f"{kind}: {caught}"
+
+
+def test_torch_recurrence_port_matches_numpy_recurrence():
+    """The torch CPU token loop (the cfg0 CPU baseline) equals the numpy fp64
+    recurrence, with and without an initial state."""
+    inp = O.synth_inputs(70, 3, 16, 16, seed=61, h0_std=0.2)
+    t = {n: torch.from_numpy(a[0]).double() for n, a in inp.items() if n != "h0"}
+    o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], h0=inp["h0"])
+    o, h = OT.recurrent_gdn2_torch(t["q"], t["k"], t["v"], t["g"], t["beta"], h0=torch.from_numpy(inp["h0"][0]),
+                                   dtype=torch.float64)
+    assert O.max_rel_err(o.numpy(), o_ref[0]) < 1e-12 and O.max_rel_err(h.numpy(), h_ref[0]) < 1e-12
+    o0, _ = OT.recurrent_gdn2_torch(t["q"], t["k"], t["v"], t["g"], t["beta"], dtype=torch.float64)
+    o0_ref, _ = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"])
+    assert O.max_rel_err(o0.numpy(), o0_ref[0]) < 1e-12
