@@ -109,6 +109,16 @@ __device__ __forceinline__ float row_inclusive_scan(float x) {
   return x;
 }
 
+// Max over the 16 lanes of each row for non-negative x, in lane 15 of the row
+// (row-shift DPP steps shift in 0 at the row start); VALU only, no LDS traffic.
+__device__ __forceinline__ float row_max_nonneg(float x) {
+  x = fmaxf(x, dpp_row_shr<1>(x));
+  x = fmaxf(x, dpp_row_shr<2>(x));
+  x = fmaxf(x, dpp_row_shr<4>(x));
+  x = fmaxf(x, dpp_row_shr<8>(x));
+  return x;
+}
+
 // Wave64 sum reduction (all lanes receive the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -88,6 +88,10 @@ __device__ __forceinline__ int value_exponent(float m) {
   return e > 0 ? e : 0;
 }
 
+// 2^e for -126 <= e <= 127, built from the exponent bits (exact; with a
+// uniform e the compiler keeps it in scalar registers)
+__device__ __forceinline__ float pow2_exact(int e) { return __builtin_bit_cast(float, (127 + e) << 23); }
+
 __host__ __device__ constexpr int wy_passes(int K) { return K > 256 ? K / 256 : 1; }
 
 struct WyLayout {

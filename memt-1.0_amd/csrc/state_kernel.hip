@@ -128,10 +128,11 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
-  // reduction steps whose f16(S) operands are read in one LDS batch (at most 16
-  // operands; one step at d = 512, whose registers are already full)
-  constexpr int SG = K > 256 ? 1 : KS * CT <= 16 ? KS : 16 / CT;
-  static_assert(KS % SG == 0, "operand batches");
+  // Up to d = 128 all f16(S) operands of a chunk (16 at most) are read from LDS
+  // in one batch before the chunk's MFMAs; the wider slices keep one read per
+  // step, interleaved by the compiler (their registers are fuller, and batching
+  // there measured slower).
+  constexpr bool BATCH = K <= 128 && KS * CT <= 16;
   constexpr int SKP = K + kSPad;  // pitch of column-major f16(S)
   constexpr int VNP = C + kVPad;  // pitch of column-major f16(V_new)
   static_assert(MODE == 0 || !CAUSAL, "the transition modes write no output");
@@ -163,38 +164,28 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   const int lcol0 = half * (NC / 2);  // first column of this wave in the LDS tiles
   const int col0 = cbase + lcol0;     // and in the state
 
-  // S tile (rt, ct): rows 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr
-  f32x4 S[RT][CT];
-  // Every group of a multi-group sequence starts from the combine's S0 (the
-  // first one from the combine's copy of h0), so when ht and h0 name the same
-  // slot the last group's ht write cannot overtake the first group's h0 read.
-  if (MODE == 0 && !(first && last)) {
-    // the group's start state from the combine, in C-frag order
-    const float* s0 = a.grp.S0 + ((size_t)unitg * H + h) * K * V;
+  // The starting state of this workgroup's slice, tile (rt, ct): rows
+  // 16 (q RT + rt) + 4 lg + e, column col0 + 16 ct + lr.  Every group of a
+  // multi-group sequence starts from the combine's S0 (the first one from the
+  // combine's copy of h0), so when ht and h0 name the same slot the last
+  // group's ht write cannot overtake the first group's h0 read.
+  const bool from_s0 = MODE == 0 && !(first && last);
+  const float* s0 = a.grp.S0 + ((size_t)unitg * H + h) * K * V;  // C-frag order (from_s0)
+  const int slot = (!from_s0 && a.h0_slot) ? a.h0_slot[seq] : seq;
+  const float* h0p = (MODE == 0 && a.h0 != nullptr) ? a.h0 + ((size_t)slot * H + h) * K * V : nullptr;
+  auto start_tile = [&](int rt, int ct) {
+    if (from_s0)
+      return *(const f32x4*)(s0 + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
+    f32x4 r;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        S[rt][ct] = *(const f32x4*)(s0 + ((size_t)((q * RT + rt) * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
-  } else {
-    const int slot = a.h0_slot ? a.h0_slot[seq] : seq;
-    const float* h0p = (MODE == 0 && a.h0 != nullptr) ? a.h0 + ((size_t)slot * H + h) * K * V : nullptr;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = 16 * (q * RT + rt) + 4 * lg + e;
-          const int col = col0 + 16 * ct + lr;
-          if constexpr (MODE == 1) S[rt][ct][e] = row == col ? 1.f : 0.f;
-          else S[rt][ct][e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
-        }
-  }
-  // settle the initial-state loads here: otherwise every later use of S in the
-  // loop would wait for all outstanding loads, prefetches included
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  asm volatile("" ::: "memory");
+    for (int e = 0; e < 4; ++e) {
+      const int row = 16 * (q * RT + rt) + 4 * lg + e;
+      const int col = col0 + 16 * ct + lr;
+      if constexpr (MODE == 1) r[e] = row == col ? 1.f : 0.f;
+      else r[e] = h0p ? h0p[(size_t)row * V + col] : 0.f;
+    }
+    return r;
+  };
 
   // channel pass of this workgroup's value columns (d = 512: two passes of 256)
   constexpr int NPU = wy_passes(K);
@@ -203,6 +194,9 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   // exponents and of its starting state's, so that U * 2^-ew and S * 2^-ew
   // stay inside the f16 operand range.  The columns of S are independent, so
   // every workgroup may use its own.  The transition (MODE 1) is scale-free.
+  // It is formed before the state is held (the starting slice is read once for
+  // its max, then again as the state), which keeps the register peak of the
+  // widest slices where it was.
   int ew = 0;
   if constexpr (MODE != 1) {
     int eu = 0;
@@ -216,9 +210,11 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
+      for (int ct = 0; ct < CT; ++ct) {
+        const f32x4 x = start_tile(rt, ct);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) smax = fmaxf(smax, fabsf(S[rt][ct][e]));
+        for (int e = 0; e < 4; ++e) smax = fmaxf(smax, fabsf(x[e]));
+      }
     smax = wave_max(smax);
     float* red = (float*)Vn_lds;  // free until the first chunk's V_new
     if (lane == 0) red[w] = smax;
@@ -227,17 +223,22 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
     for (int i = 0; i < kScanThreads / 64; ++i) m = fmaxf(m, red[i]);
     ew = __builtin_amdgcn_readfirstlane(max(eu, value_exponent(m)));
-    if (ew > 0) {
-      const float sc = ldexpf(1.f, -ew);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) S[rt][ct][e] *= sc;
-    }
   }
-  const float oscale = ldexpf(1.f, ew);  // back to the values' own scale on store
+  const float oscale = pow2_exact(ew);  // back to the values' own scale on store
+  const float iscale = pow2_exact(-ew);
+
+  f32x4 S[RT][CT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      S[rt][ct] = start_tile(rt, ct);
+      if constexpr (MODE != 1) S[rt][ct] *= iscale;
+    }
+  // settle the initial-state loads here: otherwise every later use of S in the
+  // loop would wait for all outstanding loads, prefetches included
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  asm volatile("" ::: "memory");
 
   auto write_S_lds = [&]() {
 #pragma unroll
@@ -256,20 +257,22 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   // entry to a scalar register right after its load, waiting for every
   // outstanding prefetch; this way the wait comes once per 64 chunks.
   int mbase = c_begin - 64;
-  int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0, m_eu = 0;
-  int flags = 0, block = -1, tok0 = 0, len = 0, eu_c = 0;
+  // The chunk's U exponent rides in bits 8.. of the cached flags (the flags use
+  // bits 0-1), so it costs no register of its own.
+  int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0;
+  int flags = 0, block = -1, tok0 = 0, len = 0;
   auto meta = [&](int c) {
     if (c - mbase >= 64) {
       mbase = c;
       const int cc = c + lane;
       const bool ok = cc < c_end;
       m_flags = !ok ? 0 : a.chunk_flags ? a.chunk_flags[cc] : MEMT_GDN2_CHUNK_COMMIT;
+      if constexpr (MODE != 1) m_flags |= (ok ? a.in.uexp[((size_t)cc * H + h) * NPU + pu] : 0) << 8;
       m_block = (MODE == 0 && ok && a.snaps != nullptr && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
       if constexpr (CAUSAL) {
         m_tok0 = ok ? a.chunk_tok0[cc] : 0;
         m_len = ok ? a.chunk_len[cc] : 0;
       }
-      if constexpr (MODE != 1) m_eu = ok ? a.in.uexp[((size_t)cc * H + h) * NPU + pu] : 0;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     const int i = c - mbase;
@@ -277,7 +280,6 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
     block = __builtin_amdgcn_readlane(m_block, i);
     tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
     len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
-    eu_c = MODE != 1 ? __builtin_amdgcn_readlane(m_eu, i) : 0;
   };
 
   F f;
@@ -366,7 +368,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         }
       }
       const int cur_flags = flags, cur_tok0 = tok0, cur_len = len;
-      const float uscale = ldexpf(1.f, eu_c - ew);  // this chunk's U to the workgroup's scale (<= 1)
+      // this chunk's U to the workgroup's scale, 2^(uexp - ew) <= 1, formed in scalar registers
+      const float uscale = pow2_exact((cur_flags >> 8) - ew);
       meta(cn);
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
@@ -375,26 +378,35 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         acc[ct] = zero4();
         if constexpr (CAUSAL) acco[ct] = zero4();
       }
-      // The f16(S) operands of SG reduction steps are read from LDS in one
-      // batch ahead of their MFMAs (the scheduling barrier keeps the compiler
-      // from pairing each read with its own wait), so a batch costs one LDS
-      // latency instead of one per operand.
+      if constexpr (BATCH) {
+        // every f16(S) operand read ahead of the MFMAs (the scheduling barrier
+        // keeps the compiler from pairing each read with its own wait), so the
+        // chunk pays one LDS latency instead of one per operand
+        f16x8 sb[KS][CT];
 #pragma unroll
-      for (int s0 = 0; s0 < KS; s0 += SG) {
-        f16x8 sb[SG][CT];
+        for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int s = 0; s < SG; ++s)
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) sb[s][ct] = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s0 + s);
+          for (int ct = 0; ct < CT; ++ct) sb[s][ct] = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < SG; ++s) {
+        for (int s = 0; s < KS; ++s) {
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) {
-            acc[ct] = mfma_f16(f.w[s0 + s], sb[s][ct], acc[ct]);
-            if constexpr (CAUSAL) acco[ct] = mfma_f16(sb[s][ct], f.qg[s0 + s], acco[ct]);
+            acc[ct] = mfma_f16(f.w[s], sb[s][ct], acc[ct]);
+            if constexpr (CAUSAL) acco[ct] = mfma_f16(sb[s][ct], f.qg[s], acco[ct]);
           }
-          load_w(cn, s0 + s);  // W and qg of the next chunk, step s0 + s
+          load_w(cn, s);  // W and qg of the next chunk, step s
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            const f16x8 sb = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s);
+            acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
+            if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
+          }
+          load_w(cn, s);  // W and qg of the next chunk, step s
         }
       }
       f16x4 un[CT];

@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   __shared__ __attribute__((aligned(16))) float Ld_s[4 * 16 * LQ];
   _Float16* const xw_s = xch_s;
   __shared__ float nrm_s[RAW && NCG > 1 ? 2 * NCG * C : 1];  // per-group l2norm sums
-  __shared__ float vmax_s[NT / 64];                           // per-wave max |beta v|
+  __shared__ float vmax_s[NT / 16];                           // max |beta v| per 16-lane row
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
@@ -366,8 +366,8 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             vmax = fmaxf(vmax, fabsf((float)vraw[s][half][e] * beta_of((float)btraw[s][half][e])));
-      vmax = wave_max(vmax);
-      if (lane == 0) vmax_s[tid >> 6] = vmax;
+      vmax = row_max_nonneg(vmax);  // DPP row maxima: one partial per 16 lanes
+      if (lr == 15) vmax_s[(tid >> 6) * 4 + lg] = vmax;
     }
     lds_barrier();
 
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     if constexpr (NP == 1) {
       float m = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < NT / 64; ++w2) m = fmaxf(m, vmax_s[w2]);
+      for (int w2 = 0; w2 < NT / 16; ++w2) m = fmaxf(m, vmax_s[w2]);
       const int uexp = value_exponent(m);
       uscale = ldexpf(1.f, -uexp);
       if (tid == 0) a.out.uexp[unit] = uexp;
@@ -752,8 +752,9 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
           b4 = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
         }
       };
-      // this pass's max |beta v| first (the rows are read again below, from
-      // the cache), then its value exponent
+      // this pass's beta v in registers, its max |beta v| (DPP row maxima, one
+      // partial per 16 lanes through LDS) and then its value exponent
+      float pv[VSL][8];
       float vmax = 0.f;
 #pragma unroll
       for (int s = 0; s < VSL; ++s)
@@ -763,14 +764,17 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
           BetaRaw b4;
           load_vb(s, half, v4, b4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) vmax = fmaxf(vmax, fabsf((float)v4[e] * beta_of((float)b4[e])));
+          for (int e = 0; e < 4; ++e) {
+            pv[s][4 * half + e] = valid ? (float)v4[e] * beta_of((float)b4[e]) : 0.f;
+            vmax = fmaxf(vmax, fabsf(pv[s][4 * half + e]));
+          }
         }
-      vmax = wave_max(vmax);
-      if (lane == 0) vmax_s[tid >> 6] = vmax;
+      vmax = row_max_nonneg(vmax);
+      if (lr == 15) vmax_s[(tid >> 6) * 4 + lg] = vmax;
       lds_barrier();
       float m = 0.f;
 #pragma unroll
-      for (int w2 = 0; w2 < NT / 64; ++w2) m = fmaxf(m, vmax_s[w2]);
+      for (int w2 = 0; w2 < NT / 16; ++w2) m = fmaxf(m, vmax_s[w2]);
       const int uexp = value_exponent(m);
       const float us = ldexpf(1.f, -uexp);
       if (tid == 0) a.out.uexp[unit * NP + p] = uexp;
@@ -778,16 +782,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       for (int s = 0; s < VSL; ++s) {
         f16x8 xu8;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          bf16x4 v4;
-          BetaRaw b4;
-          load_vb(s, half, v4, b4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float bt = beta_of((float)b4[e]);
-            xu8[4 * half + e] = (_Float16)(valid ? (float)v4[e] * bt * us : 0.f);
-          }
-        }
+        for (int j = 0; j < 8; ++j) xu8[j] = (_Float16)(pv[s][j] * us);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int ct = 2 * (vgl + s) + half;
