@@ -705,7 +705,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "update step: wy_kernel, trans_kernel, combine_kernel and state_kernel, timed together per step",
+            "kernel": "update step: wy_kernel, colscan_trans_kernel, combine_kernel and colscan_state_kernel, timed together per step",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -211,6 +211,51 @@ inline size_t group_layout(size_t base, int n_chunk, int n_seq, int H, int K, in
   return o;
 }
 
+// Where global group g of the two-level scan lies: sequence n owns the groups
+// [G_n, G_n + cnt_n), cnt_n = ceil(chunks_n / L), G_n the sum over earlier
+// sequences.  One wave scans the sequences 64 at a time; every lane returns
+// the same values.
+struct GroupLoc {
+  int seq, c_begin, c_end, first_group, n_groups;
+  bool valid;
+};
+__device__ __forceinline__ GroupLoc locate_group(const int32_t* soff, int n_seq, int L, int g) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  for (int n0 = 0; n0 < n_seq; n0 += 64) {
+    const int n = n0 + lane;
+    int c0 = 0, c1 = 0, cnt = 0;
+    if (n < n_seq) {
+      c0 = soff[n];
+      c1 = soff[n + 1];
+      cnt = (c1 - c0 + L - 1) / L;
+    }
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    const int first = base + incl - cnt;
+    const unsigned long long hit = __ballot(n < n_seq && g >= first && g < first + cnt);
+    if (hit != 0) {
+      const int src = __ffsll((unsigned long long)hit) - 1;
+      GroupLoc r;
+      r.seq = n0 + src;
+      r.first_group = __shfl(first, src, 64);
+      r.n_groups = __shfl(cnt, src, 64);
+      const int sc0 = __shfl(c0, src, 64), sc1 = __shfl(c1, src, 64);
+      r.c_begin = sc0 + (g - r.first_group) * L;
+      r.c_end = min(r.c_begin + L, sc1);
+      r.valid = true;
+      return r;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  GroupLoc r{};
+  r.valid = false;
+  return r;
+}
 struct StateArgs {
   WyBuffers in;
   const int32_t* chunk_tok0;
@@ -275,6 +320,10 @@ hipError_t launch_prologue(const PrologueArgs& a, int D, bool qk, hipStream_t st
 hipError_t launch_wy(const WyArgs& a, int n_chunk, int K, int V, bool causal, bool g_cumulative,
                      bool beta_bf16, hipStream_t stream);
 hipError_t launch_state(const StateArgs& a, int K, int V, bool causal, hipStream_t stream);
+// d <= 128 column-split scan: phase 1 the group transitions (units = group bound),
+// phase 0 the scan proper (units = groups, or sequences for the plain scan).
+hipError_t launch_colscan(const StateArgs& a, int K, int V, bool causal, int phase, int units,
+                          hipStream_t stream);
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
                            int K, int V, float scale, hipStream_t stream, const int32_t* block_slot = nullptr);

@@ -1,8 +1,9 @@
-// Inter-chunk state scan of the chunked GDN-2 update.
+// Inter-chunk state scan of the chunked GDN-2 update: the wide heads
+// (d = 256 and d = 512) and the group combine of every width.  d <= 128 runs
+// the column-split scan of scan_kernel.hip around the same combine_kernel.
 //
-// One workgroup (8 waves) per (sequence or chunk group, head, column slice)
-// holds a K x NC slice of the head's fp32 state in MFMA accumulators (all V
-// columns up to d = 128, 64-column slices at d = 256 and d = 512) and walks
+// One workgroup (8 waves) per (sequence or chunk group, head, 64-column slice)
+// holds a K x 64 slice of the head's fp32 state in MFMA accumulators and walks
 // the chunks in order (models/qwen/ops/_triton/state.py:76-115):
 //
 //   snapshot S if the chunk starts a read block
@@ -58,51 +59,6 @@ constexpr int kScanThreads = 512;
 constexpr int kSPad = 4;
 constexpr int kVPad = 4;
 
-// Where global group g of the two-level scan lies: sequence n owns the groups
-// [G_n, G_n + cnt_n), cnt_n = ceil(chunks_n / L), G_n the sum over earlier
-// sequences.  One wave scans the sequences 64 at a time; every lane returns
-// the same values.
-struct GroupLoc {
-  int seq, c_begin, c_end, first_group, n_groups;
-  bool valid;
-};
-__device__ __forceinline__ GroupLoc locate_group(const int32_t* soff, int n_seq, int L, int g) {
-  const int lane = threadIdx.x & 63;
-  int base = 0;
-  for (int n0 = 0; n0 < n_seq; n0 += 64) {
-    const int n = n0 + lane;
-    int c0 = 0, c1 = 0, cnt = 0;
-    if (n < n_seq) {
-      c0 = soff[n];
-      c1 = soff[n + 1];
-      cnt = (c1 - c0 + L - 1) / L;
-    }
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += y;
-    }
-    const int first = base + incl - cnt;
-    const unsigned long long hit = __ballot(n < n_seq && g >= first && g < first + cnt);
-    if (hit != 0) {
-      const int src = __ffsll((unsigned long long)hit) - 1;
-      GroupLoc r;
-      r.seq = n0 + src;
-      r.first_group = __shfl(first, src, 64);
-      r.n_groups = __shfl(cnt, src, 64);
-      const int sc0 = __shfl(c0, src, 64), sc1 = __shfl(c1, src, 64);
-      r.c_begin = sc0 + (g - r.first_group) * L;
-      r.c_end = min(r.c_begin + L, sc1);
-      r.valid = true;
-      return r;
-    }
-    base += __shfl(incl, 63, 64);
-  }
-  GroupLoc r{};
-  r.valid = false;
-  return r;
-}
 // Groups [first, first + count) of sequence n.
 __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int L, int& first, int& count) {
   const int lane = threadIdx.x & 63;
@@ -701,6 +657,16 @@ hipError_t launch_t(const StateArgs& a, bool causal, hipStream_t stream) {
     hipLaunchKernelGGL((state_kernel<K, V, false>), dim3(a.n_seq * a.H * (V / scan_slice(V))), dim3(kScanThreads),
                        0, stream, a, a.n_seq);
     return hipGetLastError();
+  } else if constexpr (K <= 128) {
+    // d <= 128: the column-split scan (scan_kernel.hip) around the same combine
+    int units = a.n_seq;
+    if (a.group_L > 0) {
+      units = group_bound(a.n_chunk, a.n_seq, a.group_L);
+      const hipError_t e = launch_colscan(a, K, V, false, 1, units, stream);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((combine_kernel<K, V>), dim3((V / 16) * a.H * a.n_seq), dim3(256), 0, stream, a);
+    }
+    return launch_colscan(a, K, V, causal, 0, units, stream);
   } else {
     int units = a.n_seq;
     if (a.group_L > 0) {

@@ -23,7 +23,7 @@ BUILD_DIR = ROOT / "_build"
 LIB_NAME = "libmemt_gdn2.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["abi.hip", "wy_kernel.hip", "state_kernel.hip", "misc_kernels.hip", "prologue_kernel.hip", "plan.cpp"]
+SOURCES = ["abi.hip", "wy_kernel.hip", "state_kernel.hip", "scan_kernel.hip", "misc_kernels.hip", "prologue_kernel.hip", "plan.cpp"]
 ROOFS_SOURCE = "roofs.hip"
 ROOFS_PATH = PKG_DIR / "libmemt_roofs.so"
 
@@ -40,6 +40,13 @@ HIPCC_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
 ]
+
+
+# Per-source additions.  The column-split scan keeps its state in VALU-visible
+# registers (it scales and converts the state every chunk), so its MFMA
+# accumulators are allocated as VGPRs rather than AGPRs, which would need a copy
+# each way per chunk.
+EXTRA_FLAGS = {"scan_kernel.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _hipcc() -> str:
@@ -69,7 +76,7 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
     for src in SOURCES:
         obj = BUILD_DIR / (Path(src).stem + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)])
     roofs_obj = BUILD_DIR / (Path(ROOFS_SOURCE).stem + ".o")
     cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / ROOFS_SOURCE), "-o", str(roofs_obj)])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
