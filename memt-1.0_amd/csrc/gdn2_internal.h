@@ -176,18 +176,25 @@ __host__ __device__ constexpr int scan_slice(int D) { return D > 128 ? 64 : D; }
 // Chunks per group for the two-level scan (0 = plain per-sequence scan).
 // The scan runs one workgroup per (sequence or group, head, column slice).
 // Groups are used when the plain scan would occupy fewer than 256 workgroups
-// (one per CU of the MI355X) and the sequences are long; L is the smallest
-// power of two >= 4 that keeps the per-group grid within 256 workgroups.
+// (one per CU of the MI355X) and the sequences are long.  Sequence n has
+// ceil(c_n / L) groups, and sum_n ceil(c_n / L) <= ceil(n_chunk / L) + n_seq - 1,
+// so L = ceil(n_chunk / G) with G = 256 / (H slices) - (n_seq - 1) is the
+// shortest group (at least 4 chunks) whose grid fits one round of 256
+// workgroups: the scan's time is its longest group's.  (A 9 % longer second
+// round, with power-of-two groups, cost the 4-segment 65536-token update a
+// third more in the transition and scan kernels.)
 // d = 512 always runs the plain scan: its group transition (K x K fp32 per
 // head) does not fit the transition and combine kernels' register plans.
 inline int scan_group_chunks(int n_chunk, int n_seq, int H, int V) {
   if (n_seq <= 0 || n_chunk <= 0 || V > 256) return 0;
   const long hs = (long)H * (V / scan_slice(V));
   if ((long)n_seq * hs >= 256) return 0;
-  int L = 4;
-  while ((long)(n_chunk / L) * hs > 256 && L < (1 << 20)) L *= 2;
+  const long G = 256 / hs - (n_seq - 1);  // groups that fit a round
+  if (G < 2) return 0;
+  long L = ((long)n_chunk + G - 1) / G;
+  if (L < 4) L = 4;
   if (n_chunk / n_seq < 2 * L) return 0;
-  return L;
+  return (int)L;
 }
 inline int group_bound(int n_chunk, int n_seq, int L) { return n_chunk / L + n_seq + 1; }
 
