@@ -18,7 +18,8 @@
 // instruction), double-buffered: while chunk c computes from one buffer the
 // records of chunk c + 1 land in the other, and one barrier per chunk (after
 // the loads have landed and every wave is done with the buffer) hands them over.
-// U is per column and goes straight to each wave's registers, a chunk ahead.
+// U, of which each wave reads only its own columns, comes through the same
+// buffers, so the chunk loop has no global load into registers to wait for.
 //
 // Kernels:
 //   colscan_state_kernel  4 waves per (sequence or group, head): the scan with
@@ -55,21 +56,27 @@ __device__ __forceinline__ void dma16(const void* src_lane, char* dst) {
 // then the workgroup barrier
 __device__ __forceinline__ void vm_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// LDS buffer of one chunk's shared records, in fragments of 1 KiB.  Every
-// record spans a multiple of NW fragments, so the record a wave's i-th load
-// belongs to is known at compile time; the decay row (K floats) takes one slot
-// per wave, each wave loading its own copy.
+
+// LDS buffer of one chunk's records, in fragments of 1 KiB: W, kg^T, (qg and
+// Aqk for the causal output), U and the decay row.  Every record but the decay
+// row spans a multiple of NW fragments, so the record a wave's i-th load belongs
+// to is known at compile time; the decay row (K floats) takes one slot, loaded
+// by wave 0.  U comes through LDS too although each wave reads only its own
+// columns of it: with no global load into registers in the chunk loop, the
+// compiler has nothing to wait for there, and the chunk's only wait is the
+// explicit one before its barrier.
 template <int K, bool CAUSAL, bool TRANS>
 struct RecordBuf {
   static constexpr int NW = TRANS ? 8 : 4;
-  static constexpr int NFW = K / 8;  // fragments of a 64 x K f16 record
+  static constexpr int NFW = K / 8;  // fragments of a 64 x K (or 64 x V, K == V) f16 record
   static_assert(NFW % NW == 0 && 8 % 4 == 0, "records in whole rounds of waves");
   static constexpr bool OUT = CAUSAL && !TRANS;
   static constexpr int F_W = 0, F_KG = NFW;
   static constexpr int F_QG = 2 * NFW;
   static constexpr int F_AQ = F_QG + (OUT ? NFW : 0);
-  static constexpr int F_D = F_AQ + (OUT ? 8 : 0);
-  static constexpr int NF = F_D + NW;
+  static constexpr int F_U = F_AQ + (OUT ? 8 : 0);
+  static constexpr int F_D = F_U + NFW;
+  static constexpr int NF = F_D + 1;
   static constexpr int BYTES = NF * kFrag;
 };
 
@@ -80,7 +87,7 @@ __device__ __forceinline__ void stage_records(const WyBuffers& in, size_t u, cha
   using B = RecordBuf<K, CAUSAL, TRANS>;
   constexpr int NW = B::NW;
 #pragma unroll
-  for (int i = 0; i < B::NF / NW; ++i) {
+  for (int i = 0; i < B::F_D / NW; ++i) {
     const int f0 = NW * i;  // compile time: which record
     const char* src;
     if (f0 < B::F_KG) {
@@ -89,15 +96,15 @@ __device__ __forceinline__ void stage_records(const WyBuffers& in, size_t u, cha
       src = (const char*)in.kgT + (u * B::NFW + (f0 - B::F_KG) + w) * kFrag;
     } else if (B::OUT && f0 < B::F_AQ) {
       src = (const char*)in.qg + (u * B::NFW + (f0 - B::F_QG) + w) * kFrag;
-    } else if (B::OUT && f0 < B::F_D) {
+    } else if (B::OUT && f0 < B::F_U) {
       src = (const char*)in.Aqk + (u * 8 + (f0 - B::F_AQ) + w) * kFrag;
     } else {
-      // K / 4 pieces of 16 bytes; lanes past them repeat the row
-      dma16((const char*)(in.decay + u * K) + 16 * (lane % (K / 4)), buf + (B::F_D + w) * kFrag);
-      continue;
+      src = (const char*)in.U + (u * B::NFW + (f0 - B::F_U) + w) * kFrag;
     }
     dma16(src + 16 * lane, buf + (f0 + w) * kFrag);
   }
+  // K / 4 pieces of 16 bytes; lanes past them repeat the row
+  if (w == 0) dma16((const char*)(in.decay + u * K) + 16 * (lane % (K / 4)), buf + B::F_D * kFrag);
 }
 
 // Role of a wave: 0 the scan proper, 1 the columns of P_g, 2 those of Q_g.
@@ -166,23 +173,17 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
     len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
   };
 
-  char* const buf0 = lds;
-  char* const buf1 = lds + B::BYTES;
+  // two record buffers: chunk c computes from one while chunk c + 1's records
+  // land in the other (a third, with two chunks in flight, measured slower in
+  // the transition kernel: 29.5 -> 32.7 us at 16 heads, 8192 tokens, d = 128)
+  constexpr int NBUF = 2;
+  auto buf = [&](int r) { return lds + (r % NBUF) * B::BYTES; };
   if (c_begin < c_end) {
     meta_load(c_begin);
-    stage_records<K, CAUSAL, TRANS>(a.in, (size_t)c_begin * H + h, buf0, w, lane);
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j)
+      if (c_begin + j < c_end) stage_records<K, CAUSAL, TRANS>(a.in, (size_t)(c_begin + j) * H + h, buf(j), w, lane);
   }
-  // U (C-frag of token tile tq, column tile col0/16 + ct): the wave's own columns
-  f16x4 un[TQ][CT];
-  auto load_u = [&](int c) {
-#pragma unroll
-    for (int tq = 0; tq < TQ; ++tq)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        un[tq][ct] = role == 1 ? f16x4{} : *(const f16x4*)(a.in.U + ((size_t)c * H + h) * (size_t)(kChunk * V) +
-                                                          ((size_t)(tq * (V / 16) + (col0 >> 4) + ct) * 64 + lane) * 4);
-  };
-  if (c_begin < c_end) load_u(c_begin);
 
   // the starting state, tile (rt, ct): rows 16 rt + 4 lg + e, column col0 + 16 ct + lr.
   // Every group of a multi-group sequence starts from the combine's S0 (the first
@@ -241,13 +242,14 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
   vm_barrier();  // the first chunk's records are in LDS
 
   for (int c = c_begin; c < c_end; ++c) {
-    const int b = (c - c_begin) & 1;
+    const int r = c - c_begin, b = r % NBUF;
     // this lane's view of the chunk's buffer: fragment f is at + f * kFrag
     lds_cchar* const cur = (lds_cchar*)lds + b * B::BYTES + 16 * lane;
     meta(c);
     const int cur_flags = flags, cur_tok0 = tok0, cur_len = len, cur_block = block;
     // the next chunk's shared records into the other buffer
-    if (c + 1 < c_end) stage_records<K, CAUSAL, TRANS>(a.in, (size_t)(c + 1) * H + h, b ? buf0 : buf1, w, lane);
+    const bool ahead = c + NBUF - 1 < c_end;  // the records NBUF - 1 chunks ahead into the free buffer
+    if (ahead) stage_records<K, CAUSAL, TRANS>(a.in, (size_t)(c + NBUF - 1) * H + h, buf(r + NBUF - 1), w, lane);
     if constexpr (!TRANS) {
       if (cur_block >= 0 && (cur_flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
         // one per-lane pointer and constant offsets, so no per-element address
@@ -301,6 +303,14 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
     // ---- V_new = U 2^(uexp - ew) - W f16(S) ----
     f16x8 Vb[2][CT];  // f16(V_new) operands: slot j of token step s2 is token 32 s2 + 16 (j / 4) + 4 lg + j % 4
     {
+      // this wave's columns of U (C fragments, 8 bytes per lane and tile)
+      f16x4 uf[TQ][CT];
+      lds_cchar* const ub = (lds_cchar*)lds + b * B::BYTES + B::F_U * kFrag + 8 * lane + (col0 >> 4) * 512;
+#pragma unroll
+      for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          uf[tq][ct] = *(const __attribute__((address_space(3))) f16x4*)(ub + (tq * (V / 16) + ct) * 512);
       f32x4 acc[TQ][CT];
       channel_product(B::F_W, acc, false);
       const float uscale = pow2_exact((cur_flags >> 8) - ew);  // <= 1
@@ -310,11 +320,10 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float u = role == 1 ? 0.f : (float)un[tq][ct][e] * uscale;
+            const float u = role == 1 ? 0.f : (float)uf[tq][ct][e] * uscale;
             Vb[tq >> 1][ct][4 * (tq & 1) + e] = (_Float16)(u - acc[tq][ct][e]);
           }
     }
-    if (c + 1 < c_end) load_u(c + 1);  // U of the next chunk, into the registers just freed
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (OUT) {
       // o^T = f16(S)^T qg^T (tile [ct][tq] kept as [tq][ct]), then scale and
