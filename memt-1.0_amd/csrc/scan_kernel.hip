@@ -143,16 +143,18 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
 
   // ---- prologue: everything the first chunk needs is requested at once ----
   int mbase = c_begin - 64;
-  int m_flags = 0, m_block = -1, m_tok0 = 0, m_len = 0;
+  int m_flags = 0, m_uexp = 0, m_block = -1, m_tok0 = 0, m_len = 0;
   int flags = 0, block = -1, tok0 = 0, len = 0;
   // plan entries of chunks [mbase, mbase + 64), one chunk per lane, read with
-  // readlane; the chunk's U exponent rides in bits 8.. of the flags
+  // readlane; the chunk's U exponent joins bits 8.. of the flags there (not at
+  // the load, which would make the prologue wait for these loads right after
+  // issuing the first chunk's direct loads)
   auto meta_load = [&](int c) {
     mbase = c;
     const int cc = c + lane;
     const bool ok = cc < c_end;
     m_flags = !ok ? 0 : a.chunk_flags ? a.chunk_flags[cc] : MEMT_GDN2_CHUNK_COMMIT;
-    m_flags |= (ok ? a.in.uexp[(size_t)cc * H + h] : 0) << 8;
+    m_uexp = ok ? a.in.uexp[(size_t)cc * H + h] : 0;
     if constexpr (!TRANS) {
       m_block = (ok && a.snaps != nullptr && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
       if constexpr (CAUSAL) {
@@ -167,7 +169,7 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
     const int i = c - mbase;
-    flags = __builtin_amdgcn_readlane(m_flags, i);
+    flags = __builtin_amdgcn_readlane(m_flags, i) | (__builtin_amdgcn_readlane(m_uexp, i) << 8);
     block = __builtin_amdgcn_readlane(m_block, i);
     tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
     len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
