@@ -40,17 +40,24 @@
 namespace memt {
 namespace {
 
+// d = 512: the chunk's kg^T record and decay row come through LDS (direct loads
+// at the start of the chunk, read in its state update) instead of a register
+// buffer a chunk ahead: 96 VGPRs fewer, which the 64-column slice needs to stay
+// within 256 without spilling.
+__host__ __device__ constexpr bool scan_kd_lds(int K) { return K > 256; }
+
 template <int K, int NC, bool CAUSAL>
 struct ScanFrag {
   static constexpr int KS = K / 32;
   static constexpr int RT = K / 64;    // 16-row state tiles per wave
   static constexpr int CT = NC / 32;   // 16-column tiles per wave (half the columns)
+  static constexpr int RTK = scan_kd_lds(K) ? 1 : RT;
   f16x8 w[KS];
   f16x8 qg[CAUSAL ? KS : 1];
-  f16x8 kg[RT][2];
+  f16x8 kg[RTK][2];
   f16x8 aq[CAUSAL ? 2 : 1];
   f16x4 u[CT];
-  f32x4 d[RT];
+  f32x4 d[RTK];
 };
 
 constexpr int kScanThreads = 512;
@@ -58,6 +65,19 @@ constexpr int kScanThreads = 512;
 // 64 + kVPad for f16(V_new), K + kSPad for the combine's bf16 S halves.
 constexpr int kSPad = 4;
 constexpr int kVPad = 4;
+
+// One direct load: lane l's 16 bytes at src_lane land at dst + 16 l (dst uniform,
+// 16-byte aligned).  Written as inline assembly so that the compiler does not see
+// an LDS write in flight and wait for it before every later LDS read: the scan
+// waits for these loads itself, before the barrier that precedes their use.  M0
+// (the LDS base of the load; one wait state between its write and the load) is
+// set here for each load; nothing else in these kernels uses M0.
+__device__ __forceinline__ void kd_dma16(const void* src_lane, char* dst) {
+  const unsigned lds_addr = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "s"(lds_addr)
+               : "memory");
+}
 
 // Groups [first, first + count) of sequence n.
 __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int L, int& first, int& count) {
@@ -80,7 +100,7 @@ __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int 
 // hold only those columns.
 template <int K, int V, int NC, bool CAUSAL, int MODE>
 __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, int cbase, _Float16* S_lds,
-                                          _Float16* Vn_lds) {
+                                          _Float16* Vn_lds, char* kd_lds = nullptr) {
   using F = ScanFrag<K, NC, CAUSAL>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
@@ -265,13 +285,36 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
                                   ((size_t)(q * 2 + s) * 64 + lane) * 8);
     }
   };
+  constexpr bool KD_LDS = scan_kd_lds(K);
   auto load_kd = [&](int c, int rt) {
-    const size_t unit = (size_t)c * H + h;
-    const int rtile = q * RT + rt;
-    f.d[rt] = *(const f32x4*)(a.in.decay + unit * K + 16 * rtile + 4 * lg);
+    if constexpr (!KD_LDS) {
+      const size_t unit = (size_t)c * H + h;
+      const int rtile = q * RT + rt;
+      f.d[rt] = *(const f32x4*)(a.in.decay + unit * K + 16 * rtile + 4 * lg);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-      f.kg[rt][s] = *(const f16x8*)(a.in.kgT + unit * (size_t)(C * K) + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
+      for (int s = 0; s < 2; ++s)
+        f.kg[rt][s] = *(const f16x8*)(a.in.kgT + unit * (size_t)(C * K) + ((size_t)(rtile * 2 + s) * 64 + lane) * 8);
+    }
+  };
+  // KD_LDS: chunk c's kg^T record (C K halves, 2 K / 16 fragments of 1 KiB) and decay
+  // row (K floats) into kd_lds by direct loads, the fragments split over the 8 waves,
+  // the decay row's K / 256 KiB on wave 0 (which issues that many more)
+  constexpr int KD_FRAG = 2 * K / 16, KD_PER_WAVE = KD_FRAG / (kScanThreads / 64), KD_DEC = K * 4 / 1024;
+  auto stage_kd = [&](int c) {
+    if constexpr (KD_LDS) {
+      const size_t unit = (size_t)c * H + h;
+      const char* kg_src = (const char*)(a.in.kgT + unit * (size_t)(C * K));
+#pragma unroll
+      for (int i = 0; i < KD_PER_WAVE; ++i) {
+        const int fr = w * KD_PER_WAVE + i;
+        kd_dma16(kg_src + (size_t)fr * 1024 + 16 * lane, kd_lds + fr * 1024);
+      }
+      if (w == 0) {
+        const char* d_src = (const char*)(a.in.decay + unit * K);
+#pragma unroll
+        for (int i = 0; i < KD_DEC; ++i) kd_dma16(d_src + i * 1024 + 16 * lane, kd_lds + KD_FRAG * 1024 + i * 1024);
+      }
+    }
   };
   // the first chunk's fragments, in the order the loop consumes and reloads them,
   // so that its vmcnt waits stay partial from the first iteration on
@@ -327,6 +370,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       // this chunk's U to the workgroup's scale, 2^(uexp - ew) <= 1, formed in scalar registers
       const float uscale = pow2_exact((cur_flags >> 8) - ew);
       meta(cn);
+      stage_kd(c);  // KD_LDS: this chunk's kg^T and decay, landed by its state update
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
 #pragma unroll
@@ -376,6 +420,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         for (int e = 0; e < 4; ++e) vn[e] = (_Float16)((float)un[ct][e] * uscale - acc[ct][e]);
         *(f16x4*)(&Vn_lds[(lcol0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
       }
+      if constexpr (KD_LDS) {
+        // every load but the KS prefetches of the next chunk's W issued since
+        // (loads complete in issue order): this chunk's direct loads have landed
+        static_assert(!CAUSAL, "the KS-deep wait counts one W load per step");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KS) : "memory");
+      }
       lds_barrier();
 
       // ---- causal output; S = decay * S + kg^T . V_new ----
@@ -397,16 +447,33 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       const bool commit = (cur_flags & MEMT_GDN2_CHUNK_COMMIT) != 0;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        if (commit) {
+        if constexpr (KD_LDS) {
+          if (commit) {
+            const int rtile = q * RT + rt;
+            const f32x4 dv = *(const f32x4*)(kd_lds + KD_FRAG * 1024 + (16 * rtile + 4 * lg) * 4);
+            f16x8 kg2[2];
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct) {
+            for (int s = 0; s < 2; ++s) kg2[s] = *(const f16x8*)(kd_lds + (rtile * 2 + s) * 1024 + 16 * lane);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
+            for (int ct = 0; ct < CT; ++ct) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
+              for (int e = 0; e < 4; ++e) S[rt][ct][e] *= dv[e];
+#pragma unroll
+              for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(kg2[s], vb[ct][s], S[rt][ct]);
+            }
           }
+        } else {
+          if (commit) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) S[rt][ct][e] *= f.d[rt][e];
+#pragma unroll
+              for (int s = 0; s < 2; ++s) S[rt][ct] = mfma_f16(f.kg[rt][s], vb[ct][s], S[rt][ct]);
+            }
+          }
+          load_kd(cn, rt);  // decay and kg^T rows of the next chunk
         }
-        load_kd(cn, rt);  // decay and kg^T rows of the next chunk
       }
       if constexpr (CAUSAL) {
         // lane holds o[16 q + lr][col0 + 16 ct + 4 lg + e]
@@ -471,8 +538,9 @@ __global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a, int un
   constexpr int NS = scan_slice(V);
   __shared__ __attribute__((aligned(16))) _Float16 S_lds[NS * (K + kSPad)];
   __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NS * (kChunk + kVPad)];
+  __shared__ __attribute__((aligned(1024))) char kd_lds[scan_kd_lds(K) ? 2 * kChunk * K + 4 * K : 16];
   const int per = units * a.H, b = blockIdx.x % per;
-  scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds);
+  scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds, kd_lds);
 }
 
 // Phase 1 of the two-level scan: nP = (K / slice) units H blocks form P_g and
