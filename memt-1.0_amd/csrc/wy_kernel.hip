@@ -15,10 +15,18 @@
 // Register layout.  The workgroup has one or two channel groups of 4 waves;
 // wave w of a group owns tokens [16w, 16w+16) over the group's channels.  Lane
 // l holds token 16w + l%16 and, for channel step s, the 8 channels
-//   slot j -> channel c0 + 32 s + 16 (j / 4) + 4 (l / 16) + j % 4      (P-frag order)
-// of every per-token input, c0 the group's first channel.  Loaded once in that order, the registers serve
-// directly as MFMA A operands of row-block products, as B operands of the
-// transposed products, and as P-frag records of the outputs.
+//   slot j -> channel c0 + 32 s + 16 (j / 4) + 4 (l / 16) + j % 4      (P-frag order, d <= 128)
+//   slot j -> channel c0 + 32 s + 8 (l / 16) + j                       (natural order, d >= 256)
+// of every per-token input, c0 the group's first channel.  Loaded once in that
+// order, the registers serve directly as MFMA A operands of row-block products
+// (any channel order is a valid reduction order) and as B operands of the
+// transposed products.  In P-frag order they are also the qg record's fragments
+// as they stand; the natural order reads each bf16 row piece with one 16-byte
+// load (64 contiguous bytes per row and instruction instead of 32) and permutes
+// qg to P-frag order through LDS.  At d >= 256 one workgroup runs per CU and its
+// load phase is not hidden behind another's compute, so the wider loads pay
+// (an update step at 64 heads, 16384 tokens, d = 256: 2641 -> 2532 us); at
+// d = 128 they measured slower (their extra registers spill).
 //
 // Steps:
 //   cumsum    16-lane DPP row scans inside each 16-token block, block totals through LDS.
@@ -66,14 +74,16 @@ __host__ __device__ constexpr int wy_groups(int K) { return K >= 128 ? 2 : 1; }
 // waves per SIMD the register budget is sized for
 __host__ __device__ constexpr int wy_waves_per_simd(int K) { return K == 128 ? 4 : K < 128 ? 2 : 1; }
 // Identity-matrix selectors: element j of lane (lr, lg) is 1 where the slot's channel
-// is column lr of a 16-channel tile of parity `half`, so mfma(rows, sel) transposes
+// (in the register order NAT names) is column lr of a 16-channel tile of parity
+// `half`, so mfma(rows, sel) transposes
 // a 16 x 16 tile exactly into the C layout (lane: 4 consecutive tokens of one channel).
+template <bool NAT>
 __device__ __forceinline__ void transpose_selectors(int lr, int lg, f16x8 (&sel)[2]) {
 #pragma unroll
   for (int half = 0; half < 2; ++half)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const bool one = (j >> 2) == half && 4 * lg + (j & 3) == lr;
+      const bool one = NAT ? 8 * lg + j == 16 * half + lr : (j >> 2) == half && 4 * lg + (j & 3) == lr;
       sel[half][j] = (_Float16)(one ? 1.f : 0.f);
     }
 }
@@ -119,6 +129,9 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
 
   const int chunk = blockIdx.x, h = blockIdx.y, H = a.H;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  constexpr bool NAT = K >= 256;  // natural channel order in registers (see the header)
+  // first channel (within a channel step of 32) of the slots 4 half .. 4 half + 3
+  auto quad = [&](int s, int half) { return NAT ? 32 * s + 8 * lg + 4 * half : 32 * s + 16 * half + 4 * lg; };
   const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);  // token block; uniform: scalar branches
   const int cg = __builtin_amdgcn_readfirstlane(tid >> 8);          // channel group
   const int cbl = cg * (KP / NCG), vcbl = cg * (VP / NCG);         // its first channel / value column in a pass
@@ -150,7 +163,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       for (int s = 0; s < KSL; ++s)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int c0 = h * K + p * KP + cbl + 32 * s + 16 * half + 4 * lg;
+          const int c0 = h * K + p * KP + cbl + quad(s, half);
           const bf16x4 qq = *(const bf16x4*)(a.q + tr * a.q_stride + c0);
           const bf16x4 kk = *(const bf16x4*)(a.k + tr * a.k_stride + c0);
 #pragma unroll
@@ -199,7 +212,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       for (int s = 0; s < KSL; ++s)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int c0 = h * K + cb + 32 * s + 16 * half + 4 * lg;
+          const int c0 = h * K + cb + quad(s, half);
           const bf16x4 ff = *(const bf16x4*)(a.f_raw + tr * a.f_stride + c0);
           const bf16x4 bb = *(const bf16x4*)(a.decay_bias + c0);
 #pragma unroll
@@ -214,7 +227,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
         for (int s = 0; s < VSL; ++s)
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
-            const int c0 = h * V + vcb + 32 * s + 16 * half + 4 * lg;
+            const int c0 = h * V + vcb + quad(s, half);
             vraw[s][half] = *(const bf16x4*)(a.v + tr * a.v_stride + c0);
             btraw[s][half] = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + c0);
           }
@@ -224,7 +237,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       for (int s = 0; s < KSL; ++s)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int c0 = h * K + cb + 32 * s + 16 * half + 4 * lg;
+          const int c0 = h * K + cb + quad(s, half);
           const bf16x4 kk = *(const bf16x4*)(a.k + tr * a.k_stride + c0);
           const bf16x4 ee = *(const bf16x4*)(a.e_raw + tr * a.e_stride + c0);
           const bf16x4 qq = *(const bf16x4*)(a.q + tr * a.q_stride + c0);
@@ -240,38 +253,69 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const f32x4 gg = *(const f32x4*)(a.g + rowK + cb + 32 * s + 16 * half + 4 * lg);
+        const f32x4 gg = *(const f32x4*)(a.g + rowK + cb + quad(s, half));
 #pragma unroll
         for (int e = 0; e < 4; ++e) g[s][4 * half + e] = gg[e];
       }
     asm volatile("" ::: "memory");
     if constexpr (NP == 1) {  // d > 256 loads v and beta for the U product only
 #pragma unroll
-      for (int s = 0; s < VSL; ++s)
+      for (int s = 0; s < VSL; ++s) {
+        if constexpr (NAT) {
+          const int c0 = vcb + 32 * s + 8 * lg;
+          const bf16x8 v8 = *(const bf16x8*)(a.v + rowV + c0);
+          if constexpr (sizeof(BetaT) == 4) {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
-          vraw[s][half] = *(const bf16x4*)(a.v + rowV + c0);
-          btraw[s][half] = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+            for (int half = 0; half < 2; ++half)
+              btraw[s][half] = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0 + 4 * half);
+          } else {
+            const bf16x8 b8 = *(const bf16x8*)((const BetaT*)a.beta + rowV + c0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              btraw[s][0][e] = b8[e];
+              btraw[s][1][e] = b8[4 + e];
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vraw[s][0][e] = v8[e];
+            vraw[s][1][e] = v8[4 + e];
+          }
+        } else {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int c0 = vcb + quad(s, half);
+            vraw[s][half] = *(const bf16x4*)(a.v + rowV + c0);
+            btraw[s][half] = *(const BetaRaw*)((const BetaT*)a.beta + rowV + c0);
+          }
         }
+      }
     }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int s = 0; s < KSL; ++s)
+    for (int s = 0; s < KSL; ++s) {
+      if constexpr (NAT) {
+        const int c0 = cb + 32 * s + 8 * lg;
+        kraw[s] = *(const bf16x8*)(a.k + rowK + c0);
+        if constexpr (HAS_B) braw[s] = *(const bf16x8*)(a.b + rowK + c0);
+        if constexpr (CAUSAL) qraw[s] = *(const bf16x8*)(a.q + rowK + c0);
+      } else {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int c0 = cb + 32 * s + 16 * half + 4 * lg;
-        const bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
-        bf16x4 bb{}, qq{};
-        if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
-        if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
+        for (int half = 0; half < 2; ++half) {
+          const int c0 = cb + quad(s, half);
+          const bf16x4 kk = *(const bf16x4*)(a.k + rowK + c0);
+          bf16x4 bb{}, qq{};
+          if constexpr (HAS_B) bb = *(const bf16x4*)(a.b + rowK + c0);
+          if constexpr (CAUSAL) qq = *(const bf16x4*)(a.q + rowK + c0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kraw[s][4 * half + e] = kk[e];
-          if constexpr (HAS_B) braw[s][4 * half + e] = bb[e];
-          if constexpr (CAUSAL) qraw[s][4 * half + e] = qq[e];
+          for (int e = 0; e < 4; ++e) {
+            kraw[s][4 * half + e] = kk[e];
+            if constexpr (HAS_B) braw[s][4 * half + e] = bb[e];
+            if constexpr (CAUSAL) qraw[s][4 * half + e] = qq[e];
+          }
         }
       }
+    }
     }
     auto kf = [&](int s, int j) { return (float)kraw[s][j]; };
     auto bkf = [&](int s, int j) { return HAS_B ? (float)kraw[s][j] * (float)braw[s][j] : (float)kraw[s][j]; };
@@ -296,7 +340,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = cbl + 32 * s + 16 * half + 4 * lg;
+        const int c0 = cbl + quad(s, half);
         const f32x4 gkv{gk[s][4 * half], gk[s][4 * half + 1], gk[s][4 * half + 2], gk[s][4 * half + 3]};
         const f32x4 gv{g[s][4 * half], g[s][4 * half + 1], g[s][4 * half + 2], g[s][4 * half + 3]};
         if (!G_CUM && lr == 15) *(f32x4*)(&tot_s[wave * KP + c0]) = gkv;
@@ -308,7 +352,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = cbl + 32 * s + 16 * half + 4 * lg;
+        const int c0 = cbl + quad(s, half);
         if constexpr (!G_CUM) {
           f32x4 base = zero4();
           for (int w2 = 0; w2 < wave; ++w2) base += *(const f32x4*)(&tot_s[w2 * KP + c0]);
@@ -381,7 +425,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       if (tid == 0) a.out.uexp[unit] = uexp;
     }
     f16x8 sel_h[2];
-    transpose_selectors(lr, lg, sel_h);
+    transpose_selectors<NAT>(lr, lg, sel_h);
     // beta v * 2^-uexp to LDS, column-major (channel rows, token columns); read by the U product
 #pragma unroll
     for (int s = 0; s < (NP == 1 ? VSL : 0); ++s) {
@@ -455,7 +499,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
             bf16x4 o4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) o4[e] = qraw[s][4 * half + e];
-            *(bf16x4*)(qo + cb + 32 * s + 16 * half + 4 * lg) = o4;
+            *(bf16x4*)(qo + cb + quad(s, half)) = o4;
           }
       }
     }
@@ -474,7 +518,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
     for (int s = 0; s < KSL; ++s)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const f32x4 r4 = *(const f32x4*)(&fac_s[wave * KP + cbl + 32 * s + 16 * half + 4 * lg]);
+        const f32x4 r4 = *(const f32x4*)(&fac_s[wave * KP + cbl + quad(s, half)]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) span = fmaxf(span, r4[e] - gk[s][4 * half + e]);
       }
@@ -525,7 +569,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       float base[8];
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int c0 = cbl + 32 * s + 16 * half + 4 * lg;
+        const int c0 = cbl + quad(s, half);
         const f32x4 r4 = *(const f32x4*)(&fac_s[wave * KP + c0]);
         const f32x4 gw = *(const f32x4*)(&fac_s[(7 + wave) * KP + c0]);
         const f32x4 ew = *(const f32x4*)(&fac_s[(11 + wave) * KP + c0]);
@@ -557,7 +601,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
         // so their exp2s run only for such blocks)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          const int c0 = cbl + 32 * s + 16 * half + 4 * lg;
+          const int c0 = cbl + quad(s, half);
           const f32x4 lastv = *(const f32x4*)(&fac_s[15 * KP + c0]);
           const int wn = wave < 3 ? wave : 2;
           const f32x4 rn = *(const f32x4*)(&fac_s[(wn + 1) * KP + c0]);
@@ -577,8 +621,23 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
           if constexpr (CAUSAL) Qd4 = mfma_f32(kbs[j], qvs[j], Qd4);
         }
       }
-      if constexpr (CAUSAL)
-        *(f16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + sg0 + s) * 64 + lane) * 8) = qg8;
+      if constexpr (CAUSAL) {
+        f16x8 qp = qg8;
+        if constexpr (NAT) {
+          // to the scan's channel order through this wave's 1280 bytes of As_s (free
+          // until the inverse): row lr holds the 32 channels of the step at a
+          // 40-element pitch; LDS operations of one wave complete in order
+          _Float16* const qs = (_Float16*)As_s + (tid >> 6) * 640 + lr * 40;
+          *(f16x8*)(qs + 8 * lg) = qg8;
+          __builtin_amdgcn_wave_barrier();
+          asm volatile("" ::: "memory");
+          const f16x4 lo = *(const f16x4*)(qs + 4 * lg), hi = *(const f16x4*)(qs + 16 + 4 * lg);
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_wave_barrier();
+          qp = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        *(f16x8*)(a.out.qg + unit * (size_t)(C * K) + ((size_t)(wave * KS + sg0 + s) * 64 + lane) * 8) = qp;
+      }
       // kg^T to global as P-frags (rows = channels, reduction = tokens)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -596,7 +655,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
           if (I > wave + 1) {
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
-              const f32x4 dn = *(const f32x4*)(&fac_s[(4 + I - 1) * KP + cbl + 32 * s + 16 * half + 4 * lg]);
+              const f32x4 dn = *(const f32x4*)(&fac_s[(4 + I - 1) * KP + cbl + quad(s, half)]);
 #pragma unroll
               for (int e = 0; e < 4; ++e) base[4 * half + e] *= dn[e];
             }
@@ -730,7 +789,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
   // token columns), by identity transposes into this group's tiles of the pass
   auto stage_x = [&](int p) {
     f16x8 sel[2];
-    transpose_selectors(lr, lg, sel);
+    transpose_selectors<NAT>(lr, lg, sel);
 #pragma unroll
     for (int ct = 0; ct < KTL; ++ct) {
       const f32x4 tr = mfma_f16(xw8[p][ct >> 1], sel[ct & 1], zero4());
@@ -743,7 +802,7 @@ __global__ __launch_bounds__(256 * wy_groups(K), wy_waves_per_simd(K)) void wy_k
       const int vcb = p * VP + vcbl;
       const size_t tr = (size_t)(tok0 + (valid ? t : 0));
       auto load_vb = [&](int s, int half, bf16x4& v4, BetaRaw& b4) {
-        const int c0 = vcb + 32 * s + 16 * half + 4 * lg;
+        const int c0 = vcb + quad(s, half);
         if constexpr (RAW) {  // projection rows; beta = bf16(sigmoid(write logit))
           v4 = *(const bf16x4*)(a.v + tr * a.v_stride + h * V + c0);
           b4 = *(const BetaRaw*)(a.w_raw + tr * a.w_stride + h * V + c0);
