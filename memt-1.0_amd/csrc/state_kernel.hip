@@ -40,18 +40,20 @@
 namespace memt {
 namespace {
 
-// d = 512: the chunk's kg^T record and decay row come through LDS (direct loads
-// at the start of the chunk, read in its state update) instead of a register
-// buffer a chunk ahead: 96 VGPRs fewer, which the 64-column slice needs to stay
-// within 256 without spilling.
-__host__ __device__ constexpr bool scan_kd_lds(int K) { return K > 256; }
+// d >= 256, the scan proper: the chunk's kg^T record and decay row come through
+// LDS (direct loads at the start of the chunk, read in its state update) instead
+// of a register buffer a chunk ahead.  At d = 512 that is 96 VGPRs the 64-column
+// slice needs to stay within 256 without spilling (commit 3.44 -> 2.93 ms); at
+// d = 256 the causal scan's 48 (update step 2550 -> 2419 us).  The transition
+// kernels keep the register buffer.
+__host__ __device__ constexpr bool scan_kd_lds(int K) { return K > 128; }
 
-template <int K, int NC, bool CAUSAL>
+template <int K, int NC, bool CAUSAL, bool KDL>
 struct ScanFrag {
   static constexpr int KS = K / 32;
   static constexpr int RT = K / 64;    // 16-row state tiles per wave
   static constexpr int CT = NC / 32;   // 16-column tiles per wave (half the columns)
-  static constexpr int RTK = scan_kd_lds(K) ? 1 : RT;
+  static constexpr int RTK = KDL ? 1 : RT;
   f16x8 w[KS];
   f16x8 qg[CAUSAL ? KS : 1];
   f16x8 kg[RTK][2];
@@ -101,7 +103,8 @@ __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int 
 template <int K, int V, int NC, bool CAUSAL, int MODE>
 __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, int cbase, _Float16* S_lds,
                                           _Float16* Vn_lds, char* kd_lds = nullptr) {
-  using F = ScanFrag<K, NC, CAUSAL>;
+  constexpr bool KD_LDS = scan_kd_lds(K) && MODE == 0;
+  using F = ScanFrag<K, NC, CAUSAL, KD_LDS>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
   // Up to d = 128 all f16(S) operands of a chunk (16 at most) are read from LDS
@@ -285,7 +288,6 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
                                   ((size_t)(q * 2 + s) * 64 + lane) * 8);
     }
   };
-  constexpr bool KD_LDS = scan_kd_lds(K);
   auto load_kd = [&](int c, int rt) {
     if constexpr (!KD_LDS) {
       const size_t unit = (size_t)c * H + h;
@@ -421,10 +423,10 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         *(f16x4*)(&Vn_lds[(lcol0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
       }
       if constexpr (KD_LDS) {
-        // every load but the KS prefetches of the next chunk's W issued since
-        // (loads complete in issue order): this chunk's direct loads have landed
-        static_assert(!CAUSAL, "the KS-deep wait counts one W load per step");
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KS) : "memory");
+        // every load but the prefetches of the next chunk's W (and qg) issued since
+        // (one per step each; loads complete in issue order): this chunk's direct
+        // loads have landed
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CAUSAL ? 2 * KS : KS) : "memory");
       }
       lds_barrier();
 
