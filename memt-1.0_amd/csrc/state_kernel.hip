@@ -54,7 +54,8 @@ struct ScanFrag {
   static constexpr int RT = K / 64;    // 16-row state tiles per wave
   static constexpr int CT = NC / 32;   // 16-column tiles per wave (half the columns)
   static constexpr int RTK = KDL ? 1 : RT;
-  f16x8 w[KS];
+  static constexpr int KSW = (KDL && K == 256) ? 1 : KS;  // d = 256 scan proper: W through LDS
+  f16x8 w[KSW];
   f16x8 qg[CAUSAL ? KS : 1];
   f16x8 kg[RTK][2];
   f16x8 aq[CAUSAL ? 2 : 1];
@@ -102,8 +103,11 @@ __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int 
 // hold only those columns.
 template <int K, int V, int NC, bool CAUSAL, int MODE>
 __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, int cbase, _Float16* S_lds,
-                                          _Float16* Vn_lds, char* kd_lds = nullptr) {
+                                          _Float16* Vn_lds, char* kd_lds = nullptr, char* w_lds = nullptr) {
   constexpr bool KD_LDS = scan_kd_lds(K) && MODE == 0;
+  // d = 256, the scan proper: W through two LDS buffers, a chunk ahead
+  constexpr bool W_LDS = KD_LDS && K == 256;
+  constexpr int WBYTES = kChunk * K * 2, W_PER_WAVE = WBYTES / 1024 / (kScanThreads / 64);
   using F = ScanFrag<K, NC, CAUSAL, KD_LDS>;
   constexpr int C = kChunk;
   constexpr int KS = F::KS, RT = F::RT, CT = F::CT;
@@ -266,8 +270,18 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   // chunk c + 1 spread over chunk c's MFMAs instead of queueing in bursts.
   auto load_w = [&](int c, int s) {
     const size_t fo = ((size_t)c * H + h) * (size_t)(C * K) + ((size_t)(q * KS + s) * 64 + lane) * 8;
-    f.w[s] = *(const f16x8*)(a.in.W + fo);
+    if constexpr (!W_LDS) f.w[s] = *(const f16x8*)(a.in.W + fo);
     if constexpr (CAUSAL) f.qg[s] = *(const f16x8*)(a.in.qg + fo);
+  };
+  auto stage_w = [&](int c, int b) {
+    if constexpr (W_LDS) {
+      const char* src = (const char*)(a.in.W + ((size_t)c * H + h) * (size_t)(C * K));
+#pragma unroll
+      for (int i = 0; i < W_PER_WAVE; ++i) {
+        const int fr = w * W_PER_WAVE + i;
+        kd_dma16(src + (size_t)fr * 1024 + 16 * lane, w_lds + b * WBYTES + fr * 1024);
+      }
+    }
   };
   auto load_u = [&](int c) {
     if constexpr (MODE != 1) {
@@ -351,7 +365,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
   if (c_begin < c_end) {
     const int c_last = c_end - 1;
     meta(c_begin);
+    stage_w(c_begin, 0);
     load_all(c_begin);
+    if constexpr (W_LDS) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      lds_barrier();  // the first chunk's W is in LDS
+    }
     for (int c = c_begin; c < c_end; ++c) {
       const int cn = min(c + 1, c_last);
       if constexpr (MODE == 0) {
@@ -373,6 +392,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       const float uscale = pow2_exact((cur_flags >> 8) - ew);
       meta(cn);
       stage_kd(c);  // KD_LDS: this chunk's kg^T and decay, landed by its state update
+      stage_w(cn, (c - c_begin + 1) & 1);  // W_LDS: the next chunk's W into the other buffer
+      const char* const wcur = w_lds + ((c - c_begin) & 1) * WBYTES + ((size_t)(q * KS) * 64 + lane) * 16;
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
 #pragma unroll
@@ -405,7 +426,10 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) {
             const f16x8 sb = b_operand(S_lds, SKP, lcol0 + 16 * ct + lr, s);
-            acc[ct] = mfma_f16(f.w[s], sb, acc[ct]);
+            f16x8 wv;
+            if constexpr (W_LDS) wv = *(const f16x8*)(wcur + s * 1024);
+            else wv = f.w[s];
+            acc[ct] = mfma_f16(wv, sb, acc[ct]);
             if constexpr (CAUSAL) acco[ct] = mfma_f16(sb, f.qg[s], acco[ct]);
           }
           load_w(cn, s);  // W and qg of the next chunk, step s
@@ -426,7 +450,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         // every load but the prefetches of the next chunk's W (and qg) issued since
         // (one per step each; loads complete in issue order): this chunk's direct
         // loads have landed
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CAUSAL ? 2 * KS : KS) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W_LDS ? W_PER_WAVE + (CAUSAL ? KS : 0) : CAUSAL ? 2 * KS : KS)
+                     : "memory");
       }
       lds_barrier();
 
@@ -491,6 +516,11 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
           }
         }
       }
+      if constexpr (W_LDS) {
+        // the next chunk's W (issued at this chunk's start) has landed: only the
+        // qg prefetches (one per step) issued after it may still be in flight
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CAUSAL ? KS : 0) : "memory");
+      }
       write_S_lds();
       lds_barrier();
     }
@@ -541,8 +571,9 @@ __global__ __launch_bounds__(kScanThreads) void state_kernel(StateArgs a, int un
   __shared__ __attribute__((aligned(16))) _Float16 S_lds[NS * (K + kSPad)];
   __shared__ __attribute__((aligned(16))) _Float16 Vn_lds[NS * (kChunk + kVPad)];
   __shared__ __attribute__((aligned(1024))) char kd_lds[scan_kd_lds(K) ? 2 * kChunk * K + 4 * K : 16];
+  __shared__ __attribute__((aligned(1024))) char w_lds[K == 256 ? 2 * 2 * kChunk * K : 16];
   const int per = units * a.H, b = blockIdx.x % per;
-  scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds, kd_lds);
+  scan_body<K, V, NS, CAUSAL, 0>(a, b / a.H, b % a.H, NS * (blockIdx.x / per), S_lds, Vn_lds, kd_lds, w_lds);
 }
 
 // Phase 1 of the two-level scan: nP = (K / slice) units H blocks form P_g and
