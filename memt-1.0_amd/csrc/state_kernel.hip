@@ -26,8 +26,13 @@
 //
 // Prefetch: each record fragment of chunk c + 1 is loaded right after its last
 // use in chunk c (one register buffer), between the MFMAs that consume the
-// other fragments; plan entries come from a per-wave cache of 64 chunks.  Loads past the last chunk reload the last chunk, so
-// every load is unconditional and the compiler's vmcnt waits stay exact.
+// other fragments; plan entries come from a per-wave cache of 64 chunks.
+// Loads past the last chunk reload the last chunk, so every load is
+// unconditional and the compiler's vmcnt waits stay exact.  The scan proper
+// at d >= 256 takes some records through LDS instead (direct loads, waited for
+// by counted vmcnt waits): the chunk's kg^T record and decay row, issued at the
+// chunk's start and read in its state update, and at d = 256 also W, two
+// buffers a chunk ahead.
 //
 // Long sequences use a two-level scan over groups of chunks (the recurrence is
 // linear in S): the same loop first runs on [I | 0] per group to form the
@@ -393,7 +398,8 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
       meta(cn);
       stage_kd(c);  // KD_LDS: this chunk's kg^T and decay, landed by its state update
       stage_w(cn, (c - c_begin + 1) & 1);  // W_LDS: the next chunk's W into the other buffer
-      const char* const wcur = w_lds + ((c - c_begin) & 1) * WBYTES + ((size_t)(q * KS) * 64 + lane) * 16;
+      const char* const wcur =
+          W_LDS ? w_lds + ((c - c_begin) & 1) * WBYTES + ((size_t)(q * KS) * 64 + lane) * 16 : nullptr;
       // ---- V_new (token rows 16 q .. 16 q + 15) and o^T from f16(S) ----
       f32x4 acc[CT], acco[CAUSAL ? CT : 1];
 #pragma unroll
