@@ -368,7 +368,7 @@ def bench_varlen(dev, steps, warmup, T=65536, H=16, D=128, cpu=True):
     return out
 
 
-def bench_cfg0(dev, reps=200, T=512, H=4, D=64, cpu=True):
+def bench_naive_recurrence_shape(dev, reps=200, T=512, H=4, D=64, cpu=True):
     """The naive-recurrence configuration (B=1 H=4 T=512 d=64, zero initial
     state): the GPU update per call, and the reference's CPU path, the
     token-by-token fp32 recurrence in torch (oracle/gdn2_torch.py)."""
@@ -676,7 +676,7 @@ def main():
     ro = bench_readout(dev, args.steps, args.warmup)
     pro = bench_prologue(dev)
     dec = bench_block_decode(dev)
-    cfg0 = bench_cfg0(dev, cpu=not args.no_cpu)
+    naive = bench_naive_recurrence_shape(dev, cpu=not args.no_cpu)
 
     causal = args.mode == "causal"
     up_traffic, ro_traffic = profiled_traffic()
@@ -734,7 +734,7 @@ def main():
     }
     result["memory_block_commit"] = pro
     result["memory_block_decode"] = dec
-    result["naive_recurrence_config"] = cfg0
+    result["naive_recurrence_config"] = naive
     result["measured_roofs"] = roofs
     result["roofline"]["mfma_frac_of_measured"] = uf / t_up / 1e12 / roofs["mfma_bf16_tflops"]
     if snap is not None:

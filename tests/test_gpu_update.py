@@ -170,12 +170,12 @@ def test_full_size_workload_heads(dev):
         assert O.max_rel_err(ht[0, h], h_ref[h].numpy()) <= TOL, h
 
 
-def test_cfg0_shape_vs_recurrence(dev):
+def test_h4_t512_d64_vs_recurrence(dev):
     """The naive-recurrence configuration's exact shape (B=1, H=4, T=512, d=64,
     zero initial state), seeded as the benchmark seeds it, in causal and
     snapshot modes, against the fp64 token recurrence."""
     T, H, D = 512, 4, 64
-    print("cfg0 shape B=1 H=4 T=512 D=64", flush=True)
+    print("naive-recurrence shape B=1 H=4 T=512 D=64", flush=True)
     t = workload_inputs(T, H, D, seed=20261201, h0_std=0.0)
     args = [t[n].to(dev) for n in ("q", "k", "v", "g", "beta")]
     ins = {n: t[n].float().numpy() for n in ("q", "k", "v", "g", "beta")}

@@ -443,8 +443,9 @@ def test_planted_mistakes_are_caught(kind):
 
 
 def test_torch_recurrence_port_matches_numpy_recurrence():
-    """The torch CPU token loop (the cfg0 CPU baseline) equals the numpy fp64
-    recurrence, with and without an initial state."""
+    """The torch CPU token loop (the CPU baseline of the B=1 H=4 T=512 d=64
+    benchmark) equals the numpy fp64 recurrence, with and without an initial
+    state."""
     inp = O.synth_inputs(70, 3, 16, 16, seed=61, h0_std=0.2)
     t = {n: torch.from_numpy(a[0]).double() for n, a in inp.items() if n != "h0"}
     o_ref, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], h0=inp["h0"])
