@@ -202,7 +202,7 @@ def _segment_lengths(total, n, seed):
 
 def test_varlen_full_size_workload(dev):
     """4 packed segments summing to 65536 tokens, H=16, d=128, per-segment
-    initial states: two heads of every segment against the fp64 chunked torch
+    initial states: every head of every segment against the fp64 chunked torch
     oracle, and every head's final state against each segment run alone."""
     from oracle.gdn2_torch import chunked_gdn2_torch
 
