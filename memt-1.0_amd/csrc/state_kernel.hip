@@ -453,9 +453,10 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
         *(f16x4*)(&Vn_lds[(lcol0 + 16 * ct + lr) * VNP + 16 * q + 4 * lg]) = vn;
       }
       if constexpr (KD_LDS) {
-        // every load but the prefetches of the next chunk's W (and qg) issued since
-        // (one per step each; loads complete in issue order): this chunk's direct
-        // loads have landed
+        // at most the next chunk's W and qg prefetches issued since are left in
+        // flight (one per step each; loads complete in issue order), so this
+        // chunk's direct loads have landed; the U prefetches issued after them are
+        // waited for too (leaving those two in flight as well measured the same)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(W_LDS ? W_PER_WAVE + (CAUSAL ? KS : 0) : CAUSAL ? 2 * KS : KS)
                      : "memory");
       }
