@@ -167,6 +167,9 @@ size_t memt_gdn2_chunk_update_workspace_size(int n_chunk, int n_seq, int H, int 
  * K, V in {64, 128, 256, 512} with K == V; at 512 only MEMT_GDN2_OUT_NONE and
  * MEMT_GDN2_OUT_SNAPSHOT (no causal output).  The workspace must hold
  * memt_gdn2_chunk_update_workspace_size(...) bytes, 256-byte aligned.
+ * At K <= 128 the SNAPSHOT read runs inside the state scan when neither ht nor
+ * snaps overlaps read_states, and as its own pass ahead of the update otherwise;
+ * the output is the same either way, bit for bit.
  */
 int memt_gdn2_chunk_update(const void* q, const void* k, const void* v, const float* g,
                            const void* beta, int beta_dtype, const void* b, const float* h0,

@@ -162,7 +162,20 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   hipStream_t st = (hipStream_t)stream;
   const WyBuffers buf = wy_buffers(workspace, lay, causal);
 
-  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x == nullptr) {
+  // d <= 128, snapshot mode: the column-split scan runs the read itself (it reads
+  // q_hat with its records and the read state once per workgroup), unless a
+  // workgroup of that launch may write the read states: pool slots (whose
+  // values the host does not see), snapshots, or final states that overlap them.
+  const size_t state_bytes = (size_t)H * K * V * sizeof(float);
+  auto overlaps = [](const void* p, size_t np, const void* r, size_t nr) {
+    return p != nullptr && r != nullptr && (const char*)p < (const char*)r + nr && (const char*)r < (const char*)p + np;
+  };
+  const bool fuse_read = out_mode == MEMT_GDN2_OUT_SNAPSHOT && K == V && K <= 128 && plan->n_chunk > 0 &&
+                         read_slot == nullptr && ht_slot == nullptr && snaps == nullptr &&
+                         !overlaps(read_states, (size_t)plan->n_block * state_bytes, ht,
+                                   (size_t)plan->n_seq * state_bytes);
+
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x == nullptr && !fuse_read) {
     // before the scan: with slots, the read may name the slot the update overwrites
     hipError_t e = launch_read_fwd((const __bf16*)q, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
                                    plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st, read_slot);
@@ -199,7 +212,7 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   }
   hipError_t e = launch_wy(wa, plan->n_chunk, K, V, causal, false, beta_dtype == MEMT_GDN2_BF16, st);
   if (e != hipSuccess) return MEMT_GDN2_ELAUNCH;
-  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x != nullptr) {
+  if (out_mode == MEMT_GDN2_OUT_SNAPSHOT && x != nullptr && !fuse_read) {
     // q_hat comes from the WY kernel; the read still precedes the scan
     e = launch_read_fwd((const __bf16*)q_hat, read_states, (__bf16*)o, plan->chunk_tok0, plan->chunk_len,
                         plan->chunk_block_ids, plan->n_chunk, H, K, V, scale, st, read_slot);
@@ -218,7 +231,11 @@ int chunk_update(const void* q, const void* k, const void* v, const float* g, co
   sa.h0_slot = h0 ? h0_slot : nullptr;
   sa.ht_slot = ht ? ht_slot : nullptr;
   sa.snaps = snaps;
-  sa.o = causal ? (__bf16*)o : nullptr;
+  sa.o = (causal || fuse_read) ? (__bf16*)o : nullptr;
+  if (fuse_read) {
+    sa.rd_states = read_states;
+    sa.rd_q = (const __bf16*)(x != nullptr ? q_hat : q);
+  }
   sa.H = H;
   sa.n_seq = plan->n_seq;
   sa.n_chunk = plan->n_chunk;

@@ -275,7 +275,11 @@ struct StateArgs {
   const int32_t* h0_slot;  // [N] or null
   const int32_t* ht_slot;  // [N] or null
   float* snaps;        // [n_block,H,K,V] or null
-  __bf16* o;           // [T,H,V] (causal) or null
+  __bf16* o;           // [T,H,V] (causal output, or the fused snapshot read) or null
+  // d <= 128, snapshot mode: the read o = bf16(scale * q_hat . bf16(rd_states[block]))
+  // runs inside the scan when rd_states is set (never written by the same launch)
+  const float* rd_states;  // [n_block,H,K,V] or null
+  const __bf16* rd_q;      // q_hat [T,H,K]
   int H;
   int n_seq;
   int n_chunk;

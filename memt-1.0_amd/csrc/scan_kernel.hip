@@ -21,6 +21,16 @@
 // U, of which each wave reads only its own columns, comes through the same
 // buffers, so the chunk loop has no global load into registers to wait for.
 //
+// In snapshot mode (every token reads the state its read block starts from,
+// read_states[block], not the evolving S) the read runs here too when the
+// launch writes no read state: each chunk's q_hat rows ride in the record
+// buffers (16-byte slots at a pitch of K / 8 + 1 slots, so the rows of an
+// operand read fall on distinct LDS banks), each wave holds bf16 of its columns
+// of the read state as MFMA operands, and o^T = bf16(S_read)^T q_hat^T is one
+// bf16 MFMA product per chunk with read_fwd_kernel's operand slots and step
+// order, so o is that kernel's output bit for bit.  It replaces a separate pass
+// that read q_hat and the state tile again.
+//
 // Kernels:
 //   colscan_state_kernel  4 waves per (sequence or group, head): the scan with
 //                         its outputs (o, snapshots, ht)
@@ -65,7 +75,11 @@ __device__ __forceinline__ void vm_barrier() { asm volatile("s_waitcnt vmcnt(0) 
 // columns of it: with no global load into registers in the chunk loop, the
 // compiler has nothing to wait for there, and the chunk's only wait is the
 // explicit one before its barrier.
-template <int K, bool CAUSAL, bool TRANS>
+// RD: the snapshot read runs inside the scan, and the buffer also holds the
+// chunk's q_hat rows after the decay row, in 16-byte slots at a pitch of K / 8 + 1
+// slots per row (the spare slot puts the 16 rows an operand read touches on
+// distinct LDS banks), in whole rounds of the NW waves' direct loads.
+template <int K, bool CAUSAL, bool TRANS, bool RD = false>
 struct RecordBuf {
   static constexpr int NW = TRANS ? 8 : 4;
   static constexpr int NFW = K / 8;  // fragments of a 64 x K (or 64 x V, K == V) f16 record
@@ -76,15 +90,18 @@ struct RecordBuf {
   static constexpr int F_AQ = F_QG + (OUT ? NFW : 0);
   static constexpr int F_U = F_AQ + (OUT ? 8 : 0);
   static constexpr int F_D = F_U + NFW;
-  static constexpr int NF = F_D + 1;
+  static constexpr int QSPR = K / 8 + 1;  // slots of one q_hat row
+  static constexpr int F_Q = F_D + 1;
+  static constexpr int NFQ = RD ? (kChunk * QSPR + 64 * NW - 1) / (64 * NW) * NW : 0;
+  static constexpr int NF = F_Q + NFQ;
   static constexpr int BYTES = NF * kFrag;
 };
 
 // Issue the direct loads of chunk unit u's records into buf: round i of the
 // NW waves loads fragments NW i .. NW i + NW - 1, wave w the (NW i + w)-th.
-template <int K, bool CAUSAL, bool TRANS>
+template <int K, bool CAUSAL, bool TRANS, bool RD = false>
 __device__ __forceinline__ void stage_records(const WyBuffers& in, size_t u, char* buf, int w, int lane) {
-  using B = RecordBuf<K, CAUSAL, TRANS>;
+  using B = RecordBuf<K, CAUSAL, TRANS, RD>;
   constexpr int NW = B::NW;
 #pragma unroll
   for (int i = 0; i < B::F_D / NW; ++i) {
@@ -108,10 +125,11 @@ __device__ __forceinline__ void stage_records(const WyBuffers& in, size_t u, cha
 }
 
 // Role of a wave: 0 the scan proper, 1 the columns of P_g, 2 those of Q_g.
-template <int K, int V, bool CAUSAL, bool TRANS>
+template <int K, int V, bool CAUSAL, bool TRANS, bool RD = false>
 __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, char* lds) {
   static_assert(K == V && (K == 64 || K == 128), "column-split scan: K == V <= 128");
-  using B = RecordBuf<K, CAUSAL, TRANS>;
+  static_assert(!RD || (!CAUSAL && !TRANS), "the fused read is the snapshot mode's");
+  using B = RecordBuf<K, CAUSAL, TRANS, RD>;
   constexpr bool OUT = B::OUT;
   constexpr int CW = V / 4, CT = CW / 16;  // columns and 16-column tiles per wave
   constexpr int KS = K / 32, RT = K / 16;  // channel steps, 16-row tiles of the state
@@ -156,8 +174,8 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
     m_flags = !ok ? 0 : a.chunk_flags ? a.chunk_flags[cc] : MEMT_GDN2_CHUNK_COMMIT;
     m_uexp = ok ? a.in.uexp[(size_t)cc * H + h] : 0;
     if constexpr (!TRANS) {
-      m_block = (ok && a.snaps != nullptr && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
-      if constexpr (CAUSAL) {
+      m_block = (ok && (RD || a.snaps != nullptr) && a.chunk_block_ids != nullptr) ? a.chunk_block_ids[cc] : -1;
+      if constexpr (CAUSAL || RD) {
         m_tok0 = ok ? a.chunk_tok0[cc] : 0;
         m_len = ok ? a.chunk_len[cc] : 0;
       }
@@ -171,8 +189,30 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
     const int i = c - mbase;
     flags = __builtin_amdgcn_readlane(m_flags, i) | (__builtin_amdgcn_readlane(m_uexp, i) << 8);
     block = __builtin_amdgcn_readlane(m_block, i);
-    tok0 = CAUSAL ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
-    len = CAUSAL ? __builtin_amdgcn_readlane(m_len, i) : 0;
+    tok0 = (CAUSAL || RD) ? __builtin_amdgcn_readlane(m_tok0, i) : 0;
+    len = (CAUSAL || RD) ? __builtin_amdgcn_readlane(m_len, i) : 0;
+  };
+  // RD: chunk c2's q_hat rows into buffer bf by direct loads.  Slot g = 64 f + lane
+  // of fragment f holds piece g % QSPR of row g / QSPR (the spare piece repeats the
+  // row's first; rows past the chunk, and past the tile, repeat its last row).
+  auto stage_q = [&](int c2, char* bf) {
+    if constexpr (RD) {
+      int t0, ln;
+      if (c2 - mbase < 64) {
+        t0 = __builtin_amdgcn_readlane(m_tok0, c2 - mbase);
+        ln = __builtin_amdgcn_readlane(m_len, c2 - mbase);
+      } else {
+        t0 = a.chunk_tok0[c2];
+        ln = a.chunk_len[c2];
+      }
+      const __bf16* qh = a.rd_q + (size_t)h * K;
+#pragma unroll
+      for (int i = 0; i < B::NFQ / B::NW; ++i) {
+        const int f = B::NW * i + w, sg = 64 * f + lane;
+        const int row = min(sg / B::QSPR, ln - 1), piece = sg % B::QSPR;
+        dma16(qh + (size_t)(t0 + row) * H * K + 8 * (piece < K / 8 ? piece : 0), bf + (B::F_Q + f) * kFrag);
+      }
+    }
   };
 
   // two record buffers: chunk c computes from one while chunk c + 1's records
@@ -180,11 +220,31 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
   // the transition kernel: 29.5 -> 32.7 us at 16 heads, 8192 tokens, d = 128)
   constexpr int NBUF = 2;
   auto buf = [&](int r) { return lds + (r % NBUF) * B::BYTES; };
+  // RD: bf16 of the read state, the A operand of o^T = bf16(S_read)^T q_hat^T:
+  // element j of (s, ct) is S_read[32 s + 8 lg + j][col0 + 16 ct + lr]
+  bf16x8 sr[RD ? KS : 1][RD ? CT : 1];
+  int sr_block = -1;
+  auto load_sr = [&](int blk) {
+    if constexpr (RD) {
+      const float* sp = a.rd_states + ((size_t)blk * H + h) * K * V + col0 + lr;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sr[s][ct][j] = (__bf16)sp[(size_t)(32 * s + 8 * lg + j) * V + 16 * ct];
+      sr_block = blk;
+    }
+  };
   if (c_begin < c_end) {
     meta_load(c_begin);
 #pragma unroll
     for (int j = 0; j < NBUF - 1; ++j)
-      if (c_begin + j < c_end) stage_records<K, CAUSAL, TRANS>(a.in, (size_t)(c_begin + j) * H + h, buf(j), w, lane);
+      if (c_begin + j < c_end) {
+        stage_records<K, CAUSAL, TRANS, RD>(a.in, (size_t)(c_begin + j) * H + h, buf(j), w, lane);
+        stage_q(c_begin + j, buf(j));
+      }
+    if constexpr (RD) load_sr(__builtin_amdgcn_readfirstlane(a.chunk_block_ids[c_begin]));
   }
 
   // the starting state, tile (rt, ct): rows 16 rt + 4 lg + e, column col0 + 16 ct + lr.
@@ -251,9 +311,15 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
     const int cur_flags = flags, cur_tok0 = tok0, cur_len = len, cur_block = block;
     // the next chunk's shared records into the other buffer
     const bool ahead = c + NBUF - 1 < c_end;  // the records NBUF - 1 chunks ahead into the free buffer
-    if (ahead) stage_records<K, CAUSAL, TRANS>(a.in, (size_t)(c + NBUF - 1) * H + h, buf(r + NBUF - 1), w, lane);
+    if (ahead) {
+      stage_records<K, CAUSAL, TRANS, RD>(a.in, (size_t)(c + NBUF - 1) * H + h, buf(r + NBUF - 1), w, lane);
+      stage_q(c + NBUF - 1, buf(r + NBUF - 1));
+    }
+    if constexpr (RD) {
+      if (cur_block != sr_block) load_sr(cur_block);  // a read block that starts inside the range
+    }
     if constexpr (!TRANS) {
-      if (cur_block >= 0 && (cur_flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
+      if (a.snaps != nullptr && cur_block >= 0 && (cur_flags & MEMT_GDN2_CHUNK_BLOCK_START)) {
         // one per-lane pointer and constant offsets, so no per-element address
         // stays live across the loop
         float* sn = a.snaps + ((size_t)cur_block * H + h) * K * V + 4 * lg * V + col0 + lr;
@@ -355,6 +421,36 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (RD) {
+      // ---- the snapshot read: o^T = bf16(S_read)^T q_hat^T, lane holds
+      // o[16 tq + lr][col0 + 16 ct + 4 lg + e]; the operands' slots and the order
+      // over the channel steps are read_fwd_kernel's, so the values are its bits
+      lds_cchar* const qb = (lds_cchar*)lds + b * B::BYTES + B::F_Q * kFrag + (lr * B::QSPR + lg) * 16;
+#pragma unroll
+      for (int tq = 0; tq < TQ; ++tq) {
+        f32x4 acc[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = zero4();
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 qv = *(const __attribute__((address_space(3))) bf16x8*)(qb + (16 * tq * B::QSPR + 4 * s) * 16);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) acc[ct] = mfma_bf16(sr[s][ct], qv, acc[ct]);
+        }
+        const int t = 16 * tq + lr;
+        if (t < cur_len) {
+          __bf16* orow = a.o + ((size_t)(cur_tok0 + t) * H + h) * V + col0 + 4 * lg;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            bf16x4 o4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = (__bf16)(acc[ct][e] * a.scale);
+            *(bf16x4*)(orow + 16 * ct) = o4;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // ---- S = decay S + kg^T f16(V_new), by 16-row tile ----
     if (cur_flags & MEMT_GDN2_CHUNK_COMMIT) {
       f16x8 kf[2][2];
@@ -436,18 +532,18 @@ __device__ __forceinline__ void colscan(const StateArgs& a, int unitg, int h, ch
   }
 }
 
-template <int K, bool CAUSAL, bool TRANS>
+template <int K, bool CAUSAL, bool TRANS, bool RD = false>
 constexpr int colscan_lds() {
-  constexpr int rec = 2 * RecordBuf<K, CAUSAL, TRANS>::BYTES;
+  constexpr int rec = 2 * RecordBuf<K, CAUSAL, TRANS, RD>::BYTES;
   constexpr int pst = TRANS ? K * (K + 4) * 4 : 0;
   return rec > pst ? rec : pst;
 }
 
 // One workgroup per (sequence or group, head): blocks b = unit * H + head.
-template <int K, int V, bool CAUSAL>
+template <int K, int V, bool CAUSAL, bool RD = false>
 __global__ __launch_bounds__(256) void colscan_state_kernel(StateArgs a) {
-  __shared__ __attribute__((aligned(1024))) char lds[colscan_lds<K, CAUSAL, false>()];
-  colscan<K, V, CAUSAL, false>(a, blockIdx.x / a.H, blockIdx.x % a.H, lds);
+  __shared__ __attribute__((aligned(1024))) char lds[colscan_lds<K, CAUSAL, false, RD>()];
+  colscan<K, V, CAUSAL, false, RD>(a, blockIdx.x / a.H, blockIdx.x % a.H, lds);
 }
 
 template <int K, int V>
@@ -463,10 +559,12 @@ hipError_t launch_colscan(const StateArgs& a, int K, int V, bool causal, int pha
   if (K == 128 && V == 128) {
     if (phase == 1) hipLaunchKernelGGL((colscan_trans_kernel<128, 128>), grid, dim3(512), 0, stream, a);
     else if (causal) hipLaunchKernelGGL((colscan_state_kernel<128, 128, true>), grid, dim3(256), 0, stream, a);
+    else if (a.rd_states) hipLaunchKernelGGL((colscan_state_kernel<128, 128, false, true>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((colscan_state_kernel<128, 128, false>), grid, dim3(256), 0, stream, a);
   } else if (K == 64 && V == 64) {
     if (phase == 1) hipLaunchKernelGGL((colscan_trans_kernel<64, 64>), grid, dim3(512), 0, stream, a);
     else if (causal) hipLaunchKernelGGL((colscan_state_kernel<64, 64, true>), grid, dim3(256), 0, stream, a);
+    else if (a.rd_states) hipLaunchKernelGGL((colscan_state_kernel<64, 64, false, true>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((colscan_state_kernel<64, 64, false>), grid, dim3(256), 0, stream, a);
   } else {
     return hipErrorInvalidValue;

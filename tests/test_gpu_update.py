@@ -67,6 +67,30 @@ def test_token_memory_packed(dev):
     assert O.parity_err(host(read), r_ref, out_bf16=True) <= TOL
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("lengths", [[130, 1, 129], [5000, 3, 2300], [64]])
+def test_snapshot_read_in_scan_equals_reader(dev, D, lengths):
+    """At d <= 128 the snapshot-mode read runs inside the scan kernel; its
+    output must be the standalone reader's bit for bit (same operand rounding,
+    slot order and step order), on the plain and the two-level scan, and the
+    oracle's within the tolerance."""
+    print(f"fused snapshot read D={D} lengths={lengths}", flush=True)
+    H, N = 2, len(lengths)
+    T = sum(lengths)
+    inp = O.synth_inputs(T, H, D, D, seed=41 + D + T, h0_std=0.05, n_seq=N)
+    rs = (np.random.default_rng(42 + T).standard_normal((N, H, D, D)) * 0.05).astype(np.float32)
+    q, k, v, g, _, ws = _dev_inputs(inp, dev)
+    beta = O.bf16_round(inp["beta"])
+    rs_d = to_dev(rs, dev)
+    read, final = memt_gdn2.token_memory_packed(q, k, v, g, bf(beta, dev), rs_d, ws, erase=None,
+                                                lengths=lengths, scale=D ** -0.5, chunk_tokens=2048)
+    alone = memt_gdn2.snapshot_read(q, rs_d, lengths, D ** -0.5, bf16_accumulator_output=True)
+    torch.cuda.synchronize()
+    assert torch.equal(read, alone)
+    r_ref = O.snapshot_read(inp["q"], rs, lengths, D ** -0.5)
+    assert O.parity_err(host(read), r_ref, out_bf16=True) <= TOL
+
+
 def test_snapshot_mode_and_no_initial_state(dev):
     T, H, D = 100, 2, 64
     inp = O.synth_inputs(T, H, D, D, seed=31)
