@@ -278,8 +278,10 @@ def _chunk_update(q, k, v, g, beta, b, h0, read_states, plan: ChunkPlan, scale: 
             raise ValueError(f"{name} must be {dt}, got {t.dtype}")
     if beta.dtype not in _DT:
         raise ValueError("write gate must be bf16 or fp32")
-    expected = (plan.num_sample, H, K, V)
-    for name, t in (("write_states", h0), ("read_states", read_states)):
+    # write states per sample, read states per read block (one per sample in
+    # the packed commit, whose samples are its read blocks)
+    for name, t, rows in (("write_states", h0, plan.num_sample), ("read_states", read_states, plan.num_block)):
+        expected = (rows, H, K, V)
         if t is not None and (tuple(t.shape) != expected or t.dtype != torch.float32):
             raise ValueError(f"{name} must be fp32 {expected}")
     q, k, v, g, beta, b, h0, read_states = _contig(q, k, v, g, beta, b, h0, read_states)

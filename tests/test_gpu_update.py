@@ -91,6 +91,39 @@ def test_snapshot_read_in_scan_equals_reader(dev, D, lengths):
     assert O.parity_err(host(read), r_ref, out_bf16=True) <= TOL
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_snapshot_read_in_scan_with_read_blocks_inside_a_sample(dev, D):
+    """Read boundaries inside a sample (turns): the scan's read changes its
+    state where the read block changes, on the plain and the two-level scan;
+    bit for bit the standalone reader's output on the same plan."""
+    from memt_gdn2.layout import build_chunk_plan
+    from memt_gdn2.ops import _chunk_update
+
+    H = 2
+    for T, reads in ((400, [0, 70, 130, 131, 400]), (6000, [0, 700, 1900, 4100, 6000])):
+        print(f"read blocks inside a sample D={D} T={T} reads={reads}", flush=True)
+        inp = O.synth_inputs(T, H, D, D, seed=51 + T + D, h0_std=0.05)
+        nb = len(reads) - 1
+        rs = (np.random.default_rng(52 + T).standard_normal((nb, H, D, D)) * 0.05).astype(np.float32)
+        q, k, v, g, _, h0 = _dev_inputs(inp, dev)
+        beta = bf(O.bf16_round(inp["beta"]), dev)
+        rs_d = to_dev(rs, dev)
+        plan = build_chunk_plan(reads, [0, T], device=q.device)
+        o, ht = _chunk_update(q, k, v, g, beta, None, h0, rs_d, plan, D ** -0.5, "snapshot")
+        alone = memt_gdn2.memt_gdn2_read_fwd(q, rs_d, plan, D ** -0.5, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(o, alone.view_as(o))
+        qh, sb = host(q)[0].astype(np.float64), O.bf16_round(rs).astype(np.float64)
+        ref = np.zeros((T, H, D))
+        for n in range(nb):
+            a, b = reads[n], reads[n + 1]
+            ref[a:b] = np.einsum("thk,hkv->thv", qh[a:b], sb[n]) * D ** -0.5
+        assert O.parity_err(host(o)[0], ref, out_bf16=True) <= TOL
+        _, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], O.bf16_round(inp["beta"]),
+                                    h0=inp["h0"])
+        assert O.max_rel_err(host(ht), h_ref) <= TOL
+
+
 def test_snapshot_mode_and_no_initial_state(dev):
     T, H, D = 100, 2, 64
     inp = O.synth_inputs(T, H, D, D, seed=31)
