@@ -124,6 +124,31 @@ def test_snapshot_read_in_scan_with_read_blocks_inside_a_sample(dev, D):
         assert O.max_rel_err(host(ht), h_ref) <= TOL
 
 
+def test_snapshot_read_in_scan_past_the_plan_cache(dev):
+    """16 sequences x 16 heads fill the launch, so the plain scan runs and each
+    workgroup walks 66 chunks: the read's q rows for chunk 64 come from the plan
+    tables directly rather than the scan's 64-chunk cache.  Bit for bit the
+    standalone reader."""
+    H, D, N, n = 16, 64, 16, 4200
+    T = N * n
+    print(f"fused snapshot read past the plan cache T={T} H={H} D={D}", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(61)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(1, T, H, D, generator=gen, device=dev), dim=-1).to(torch.bfloat16)
+    k = nrm(torch.randn(1, T, H, D, generator=gen, device=dev), dim=-1).to(torch.bfloat16)
+    v = torch.randn(1, T, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    g = torch.nn.functional.logsigmoid(torch.randn(1, T, H, D, generator=gen, device=dev))
+    beta = torch.sigmoid(torch.randn(1, T, H, D, generator=gen, device=dev))
+    rs = torch.randn(N, H, D, D, generator=gen, device=dev) * 0.05
+    ws = torch.randn(N, H, D, D, generator=gen, device=dev) * 0.05
+    read, final = memt_gdn2.token_memory_packed(q, k, v, g, beta, rs, ws, erase=None, lengths=[n] * N,
+                                                scale=D ** -0.5, chunk_tokens=2048)
+    alone = memt_gdn2.snapshot_read(q, rs, [n] * N, D ** -0.5, bf16_accumulator_output=True)
+    torch.cuda.synchronize()
+    assert torch.equal(read, alone)
+    assert bool(torch.isfinite(final).all())
+
+
 def test_snapshot_mode_and_no_initial_state(dev):
     T, H, D = 100, 2, 64
     inp = O.synth_inputs(T, H, D, D, seed=31)
