@@ -149,6 +149,39 @@ def test_snapshot_read_in_scan_past_the_plan_cache(dev):
     assert bool(torch.isfinite(final).all())
 
 
+@pytest.mark.parametrize("T", [300, 6000])
+def test_snapshot_read_with_final_states_over_the_read_states(dev, T):
+    """memt_gdn2_chunk_update with ht naming the read states' memory: the read
+    must see the states from before the update (it then runs as its own pass,
+    not inside the scan), on the plain and the two-level scan."""
+    import ctypes
+    from memt_gdn2 import _lib
+    from memt_gdn2.layout import packed_plan
+    from memt_gdn2.ops import _DT, _OUT, _workspace, workspace_bytes
+
+    H, D = 2, 128
+    print(f"final states over the read states T={T}", flush=True)
+    inp = O.synth_inputs(T, H, D, D, seed=71 + T, h0_std=0.05)
+    q, k, v, g, _, h0 = _dev_inputs(inp, dev)
+    beta = bf(O.bf16_round(inp["beta"]), dev)
+    rs = torch.randn(1, H, D, D, generator=torch.Generator(device=dev).manual_seed(72), device=dev) * 0.05
+    before = rs.clone()
+    plan = packed_plan([T], dev, chunk_tokens=2048)
+    o = torch.empty(1, T, H, D, dtype=torch.bfloat16, device=dev)
+    ws = _workspace(dev, workspace_bytes(plan.num_chunk, H, D, D, "snapshot", plan.num_sample))
+    p = plan.abi()
+    lib = _lib.load()
+    _lib.check(lib.memt_gdn2_chunk_update(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), _DT[beta.dtype], None,
+        h0.data_ptr(), rs.data_ptr(), rs.data_ptr(), None, o.data_ptr(), ctypes.byref(p), T, H, D, D,
+        float(D ** -0.5), _OUT["snapshot"], ws.data_ptr(), ws.numel(), _lib.stream_of(dev)), "chunk_update")
+    alone = memt_gdn2.snapshot_read(q, before, [T], D ** -0.5, bf16_accumulator_output=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, alone)
+    _, h_ref = O.recurrent_gdn2(inp["q"], inp["k"], inp["v"], inp["g"], O.bf16_round(inp["beta"]), h0=inp["h0"])
+    assert O.max_rel_err(host(rs), h_ref) <= TOL
+
+
 def test_snapshot_mode_and_no_initial_state(dev):
     T, H, D = 100, 2, 64
     inp = O.synth_inputs(T, H, D, D, seed=31)
