@@ -33,6 +33,21 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// One direct load (global_load_lds_dwordx4): lane l's 16 bytes at src_lane land
+// at dst + 16 l (dst uniform over the wave, 16-byte aligned).  Written as inline
+// assembly so that the compiler does not see an LDS write in flight and wait for
+// it before every later LDS read: the caller waits for these loads itself
+// (s_waitcnt vmcnt) before the barrier that precedes their use.  M0, the LDS base
+// of the load (one wait state between its write and the load), is set for each
+// load: a kernel that calls this must use M0 for nothing else (M0 is reserved to
+// the compiler, so it cannot be declared clobbered).
+__device__ __forceinline__ void lds_dma16(const void* src_lane, char* dst) {
+  const unsigned lds_addr = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "s"(lds_addr)
+               : "memory");
+}
+
 // Native v_exp_f32 (base 2).  Inputs below -126 give denormal/zero results.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

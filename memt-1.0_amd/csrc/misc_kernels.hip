@@ -5,23 +5,17 @@ namespace memt {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Snapshot reader (models/qwen/ops/_triton/read.py:22-71): per (chunk, head),
-// o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32 accumulation.
-// A workgroup takes CB state columns (all of them up to d = 256) of one head
-// for a run of `per` consecutive chunks, and reloads the bf16 state tile only
-// when the block changes.  Wave w handles token rows [16w, 16w + 16); it
-// issues all of a chunk's q loads before its first product, so a chunk costs
-// one memory latency rather than one per 32 channels.
-// With several column tiles (d = 512), the NCB workgroups of one (run, head)
-// read the same q rows: their block indices are 8 apart, so they share an XCD
-// (blocks go to the eight XCDs round-robin) and run together, and q comes from
-// that XCD's L2 after its first read.
+// Snapshot reader (models/qwen/ops/_triton/read.py:22-71) for d <= 128: per
+// (chunk, head), o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32
+// accumulation.  A workgroup takes all V state columns of one head for a run of
+// kReadRun consecutive chunks, and reloads the bf16 state tile only when the
+// block changes.  Wave w handles token rows [16w, 16w + 16); it issues all of a
+// chunk's q loads before its first product, so a chunk costs one memory
+// latency rather than one per 32 channels.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr int read_cols(int V) { return V > 256 ? 64 : V; }
-// chunks per reader workgroup: a run shares one state tile load (d = 512, the
-// Flash commit at 64 heads and 8192 tokens: runs of 16 / 32 / 64 / 128 chunks
-// took 2857 / 2847 / 2837 / 2833 us per commit)
-__host__ __device__ constexpr int read_run(int V) { return V > 256 ? 64 : 4; }
+// chunks per reader workgroup (snapshot mode at 16 heads, 8192 tokens, d = 128:
+// runs of 1, 2, 8 or 16 chunks measured 2-17 % slower than 4)
+constexpr int kReadRun = 4;
 
 template <int K, int V>
 __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict__ q,
@@ -30,13 +24,12 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
                                                        const int32_t* chunk_len, const int32_t* block_ids,
                                                        int n_chunk, int n_units, int H, float scale,
                                                        const int32_t* block_slot) {
-  constexpr int CB = read_cols(V), NCB = V / CB, SKP = K + 8, per = read_run(V);
-  __shared__ __attribute__((aligned(16))) __bf16 S_lds[CB * SKP];  // column-major bf16(S), CB columns
-  // block b -> column tile (b / 8) % NCB of unit (b % 8) + 8 (b / (8 NCB)); a unit is (run, head)
-  const int b = blockIdx.x;
-  const int unit = NCB == 1 ? b : (b & 7) + 8 * (b / (8 * NCB));
+  constexpr int CB = V, SKP = K + 8, per = kReadRun;
+  static_assert(V <= 128, "d > 128 reads in read_wide_kernel");
+  __shared__ __attribute__((aligned(16))) __bf16 S_lds[CB * SKP];  // column-major bf16(S)
+  const int unit = blockIdx.x;  // (run, head)
   if (unit >= n_units) return;
-  const int h = unit % H, col0 = (NCB == 1 ? 0 : (b >> 3) % NCB) * CB;
+  const int h = unit % H, col0 = 0;
   const int c_begin = (unit / H) * per, c_end = min(c_begin + per, n_chunk);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   int loaded = -1;
@@ -101,6 +94,189 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
         const int tt = 16 * w + 4 * lg + e;
         if (tt < len) o[((size_t)(tok0 + tt) * H + h) * V + col0 + 16 * ct + lr] = (__bf16)(acc[ct][e] * scale);
       }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Snapshot reader for d = 256 and 512: read_fwd_kernel's product with the
+// state held in registers.  A workgroup of 8 waves takes 128 state columns of
+// one head (wave w: columns col0 + 16 w .. + 15) for a run of chunks.  Each wave
+// holds its 16 columns of bf16(S), all K channels (64 registers at d = 512), as
+// the A operand of o^T = bf16(S)^T q^T, loaded once per block, so the state is
+// read from memory once per run instead of from LDS for every 16 tokens.  The
+// q rows come through LDS by direct loads in steps of a chunk (half a chunk at
+// d = 512, so that two workgroups share a CU and one covers the other's waits),
+// double-buffered: step i + 1's rows land while step i is multiplied.  The
+// operand slots and the order of the products over the channels are
+// read_fwd_kernel's, so the output is bit-identical to it.  The NH workgroups of
+// one (run, head) read the same q rows; their block indices are 8 apart, so they
+// share an XCD and its L2 (HBM fetches at d = 512: q and the state once).
+// ---------------------------------------------------------------------------
+constexpr int kWideCols = 128;  // state columns per wide-reader workgroup
+// rows of q per step: half a chunk at d = 512, so that two workgroups fit a CU's LDS
+__host__ __device__ constexpr int wide_rows(int K) { return K > 256 ? 32 : kChunk; }
+template <int K>
+struct WideReadLds {
+  static constexpr int TS = wide_rows(K);                        // token rows per step
+  static constexpr int QSPR = K / 8 + 1;                         // 16-byte slots per q row: K / 8 and a spare
+  static constexpr int NF = (TS * QSPR * 16 + 1023) / 1024;      // direct loads (1 KiB each) per step
+  static constexpr int BYTES = NF * 1024;                        // one step's buffer
+  static constexpr int PIECE = 32 * kWideCols * 4;               // 32 state rows of the workgroup's columns, fp32
+  static constexpr int NSLOT = BYTES / PIECE;                    // state pieces a buffer holds
+};
+
+// s_waitcnt vmcnt(N) (N a constant), then the workgroup barrier
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restrict__ q,
+                                                        const float* __restrict__ snaps,
+                                                        __bf16* __restrict__ o,
+                                                        const int32_t* __restrict__ chunk_tok0,
+                                                        const int32_t* __restrict__ chunk_len,
+                                                        const int32_t* __restrict__ block_ids, int n_chunk,
+                                                        int n_units, int per, int H, float scale,
+                                                        const int32_t* __restrict__ block_slot) {
+  using L = WideReadLds<K>;
+  constexpr int NW = 8, NH = V / kWideCols, KS = K / 32, QSPR = L::QSPR, NSLOT = L::NSLOT;
+  constexpr int TS = L::TS, SPC = kChunk / TS, TT = TS / 16;  // rows per step, steps per chunk, token tiles
+  static_assert(V % kWideCols == 0 && K == V && NSLOT >= 1 && NSLOT <= 4, "square heads of 256 or 512");
+  __shared__ __attribute__((aligned(1024))) char q_lds[2 * L::BYTES];
+  // block b -> column tile (b / 8) % NH of unit (b % 8) + 8 (b / (8 NH)); a unit is (run, head)
+  const int b = blockIdx.x;
+  const int unit = (b & 7) + 8 * (b / (8 * NH));
+  if (unit >= n_units) return;
+  const int h = unit % H, tile = (b >> 3) % NH;
+  // uniform values kept in scalar registers, so the chunk table reads are scalar loads
+  const int c_begin = __builtin_amdgcn_readfirstlane((unit / H) * per);
+  const int c_end = __builtin_amdgcn_readfirstlane(min(c_begin + per, n_chunk));
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int colw = tile * kWideCols + 16 * w;  // this wave's first column
+
+  // step i (rows r0 .. r0 + TS - 1 of chunk c_begin + i / SPC, r0 = TS (i % SPC))
+  // into buffer bi: the buffer is a flat run of 16-byte slots, row r's channels
+  // 8 p .. 8 p + 7 in slot r QSPR + p; the spare slot of a row loads a copy of
+  // its first piece, rows past the chunk end its last row
+  auto stage = [&](int i, int bi) {
+    const int c = c_begin + i / SPC, r0 = TS * (i % SPC);
+    const int t0 = __builtin_amdgcn_readfirstlane(chunk_tok0[c]) + r0;
+    const int ln = __builtin_amdgcn_readfirstlane(chunk_len[c]) - r0;
+    if (ln <= 0) return;
+    const __bf16* qh = q + (size_t)h * K;
+    char* const dst = q_lds + bi * L::BYTES;
+    // the lane index, opaque so that the per-load lane offsets are formed here
+    // and not kept in registers across the step loop (spilled, their reloads
+    // would wait for the direct loads in flight)
+    int ql = lane;
+    asm volatile("" : "+v"(ql));
+#pragma unroll
+    for (int u = 0; u < (L::NF + NW - 1) / NW; ++u) {
+      const int f = NW * u + w;  // wave w: loads w, w + NW, ...
+      if (f < L::NF) {
+        const int sg = 64 * f + ql, row = min(min(sg / QSPR, TS - 1), ln - 1), piece = sg % QSPR;
+        lds_dma16(qh + (size_t)(t0 + row) * H * K + 8 * (piece < K / 8 ? piece : 0), dst + f * 1024);
+      }
+    }
+  };
+  // A operand of step s: element j is bf16(S)[32 s + 8 lg + j][colw + lr]
+  bf16x8 sr[KS];
+  // The state reaches the registers through the free q buffer: rows
+  // 32 p .. 32 p + 31 of the workgroup's 128 columns (16 KiB of fp32; one direct
+  // load of 1 KiB covers two rows, 2 per wave) go to slot p % NSLOT, and each lane
+  // then reads its 8 values of channel step p from there, with up to NSLOT - 1
+  // later pieces in flight.
+  auto load_sr = [&](int blk, char* free_buf) {
+    const float* sp = snaps + ((size_t)(block_slot ? block_slot[blk] : blk) * H + h) * K * V +
+                      (size_t)(lane >> 5) * V + tile * kWideCols + 4 * (lane & 31);
+    auto stage_piece = [&](int pc) {
+#pragma unroll
+      for (int i = 0; i < 16 / NW; ++i) {
+        const int r2 = NW * i + w;  // rows 2 r2, 2 r2 + 1 of the piece
+        lds_dma16(sp + (size_t)(32 * pc + 2 * r2) * V, free_buf + (pc % NSLOT) * L::PIECE + r2 * 1024);
+      }
+    };
+    // this lane's word of a piece: row 8 lg + j, column 16 w + lr
+    const __attribute__((address_space(3))) char* const rb =
+        (const __attribute__((address_space(3))) char*)free_buf + (8 * lg * kWideCols + 16 * w + lr) * 4;
+#pragma unroll
+    for (int pc = 0; pc < NSLOT - 1 && pc < KS; ++pc) stage_piece(pc);
+#pragma unroll
+    for (int pc = 0; pc < KS; ++pc) {
+      if (pc + NSLOT - 1 < KS) stage_piece(pc + NSLOT - 1);
+      // piece pc landed; the (2 per wave) loads of the pieces after it may still be in flight
+      const int ahead = (KS - 1 - pc < NSLOT - 1) ? KS - 1 - pc : NSLOT - 1;
+      if (ahead >= 3) vm_wait_barrier<6>();
+      else if (ahead == 2) vm_wait_barrier<4>();
+      else if (ahead == 1) vm_wait_barrier<2>();
+      else vm_wait_barrier<0>();
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        sr[pc][j] = (__bf16)*(const __attribute__((address_space(3))) float*)(rb + (pc % NSLOT) * L::PIECE +
+                                                                              j * kWideCols * 4);
+      // every wave's reads of the slot done before a later piece lands there
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+  };
+
+  const int n_steps = (c_end - c_begin) * SPC;
+  stage(0, 0);
+  vm_wait_barrier<0>();  // the first step's rows are in LDS
+  int sr_block = -1;
+  for (int i = 0; i < n_steps; ++i) {
+    const int bi = i & 1, c = c_begin + i / SPC, r0 = TS * (i % SPC);
+    const int tok0 = __builtin_amdgcn_readfirstlane(chunk_tok0[c]) + r0;
+    const int len = __builtin_amdgcn_readfirstlane(chunk_len[c]) - r0;  // rows of this step: min(len, TS)
+    const int blk = __builtin_amdgcn_readfirstlane(block_ids[c]);
+    // a new block's state, through the other buffer (free: its reads ended
+    // before the last barrier) before the next chunk's rows go there
+    if (len > 0 && blk != sr_block) {
+      load_sr(blk, q_lds + (bi ^ 1) * L::BYTES);
+      sr_block = blk;
+    }
+    // the next step's rows into the other buffer
+    if (i + 1 < n_steps) stage(i + 1, bi ^ 1);
+    f32x4 acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = zero4();
+    if (len > 0) {
+      // this lane's q operand: token 16 tt + lr, channels 32 s + 8 lg .. + 7 (its
+      // offset formed here from an opaque lane index: a value kept across the
+      // step loop would be spilled, and its reload would wait for the next
+      // step's direct loads)
+      int ml = lane;
+      asm volatile("" : "+v"(ml));
+      const __attribute__((address_space(3))) char* const qb =
+          (const __attribute__((address_space(3))) char*)q_lds + bi * L::BYTES + ((ml & 15) * QSPR + (ml >> 4)) * 16;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+          const bf16x8 qv = *(const __attribute__((address_space(3))) bf16x8*)(qb + (16 * tt * QSPR + 4 * s) * 16);
+          acc[tt] = mfma_bf16(sr[s], qv, acc[tt]);
+        }
+    }
+    // every wave's loads of the next step landed, every wave done with this buffer
+    // (the wait also covers the previous step's stores, long since issued)
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (len > 0) {
+      int sl = lane;  // opaque again: the row offsets are formed here
+      asm volatile("" : "+v"(sl));
+      __bf16* const op = o + ((size_t)tok0 * H + h) * V + colw + 4 * (sl >> 4);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const int t = 16 * tt + (sl & 15);
+        if (t < len) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (__bf16)(acc[tt][e] * scale);
+          *(bf16x4*)(op + (size_t)t * H * V) = v;
+        }
+      }
+    }
   }
 }
 
@@ -376,24 +552,47 @@ __global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const _
 
 }  // namespace
 
+// CUs of the current device, looked up once per device
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
                            const int32_t* chunk_len, const int32_t* chunk_block_ids, int n_chunk, int H,
                            int K, int V, float scale, hipStream_t stream, const int32_t* block_slot) {
   if (n_chunk == 0) return hipSuccess;
-  const int runs = (n_chunk + read_run(V) - 1) / read_run(V), n_units = runs * H;
-  // units rounded up to a multiple of 8 when a unit has several column tiles
-  const int ncb = V / read_cols(V), n_blocks = ncb == 1 ? n_units : (n_units + 7) / 8 * 8 * ncb;
 #define MEMT_RD(KK, VV)                                                                                        \
   if (K == KK && V == VV) {                                                                                    \
-    hipLaunchKernelGGL((read_fwd_kernel<KK, VV>), dim3(n_blocks), dim3(256), 0, stream, q, snaps, o, chunk_tok0, \
+    const int n_units = (n_chunk + kReadRun - 1) / kReadRun * H;                                               \
+    hipLaunchKernelGGL((read_fwd_kernel<KK, VV>), dim3(n_units), dim3(256), 0, stream, q, snaps, o, chunk_tok0,  \
                        chunk_len, chunk_block_ids, n_chunk, n_units, H, scale, block_slot);                    \
     return hipGetLastError();                                                                                  \
   }
   MEMT_RD(64, 64)
   MEMT_RD(128, 128)
-  MEMT_RD(256, 256)
-  MEMT_RD(512, 512)
 #undef MEMT_RD
+  if (K == V && (K == 256 || K == 512)) {
+    // runs sized so the grid fills the chip once, two workgroups per CU (66 KB of LDS each)
+    const int nh = V / kWideCols, per_run = H * nh, slots = device_cus() * 2;
+    const int runs_wanted = (slots + per_run - 1) / per_run;  // at least 1
+    const int per = (n_chunk + runs_wanted - 1) / runs_wanted;
+    const int n_units = (n_chunk + per - 1) / per * H;
+    const int n_blocks = (n_units + 7) / 8 * 8 * nh;
+    if (K == 256)
+      hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(512), 0, stream, q, snaps, o,
+                         chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
+    else
+      hipLaunchKernelGGL((read_wide_kernel<512, 512>), dim3(n_blocks), dim3(512), 0, stream, q, snaps, o,
+                         chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
+    return hipGetLastError();
+  }
   return hipErrorInvalidValue;
 }
 

@@ -74,19 +74,6 @@ constexpr int kScanThreads = 512;
 constexpr int kSPad = 4;
 constexpr int kVPad = 4;
 
-// One direct load: lane l's 16 bytes at src_lane land at dst + 16 l (dst uniform,
-// 16-byte aligned).  Written as inline assembly so that the compiler does not see
-// an LDS write in flight and wait for it before every later LDS read: the scan
-// waits for these loads itself, before the barrier that precedes their use.  M0
-// (the LDS base of the load; one wait state between its write and the load) is
-// set here for each load; nothing else in these kernels uses M0.
-__device__ __forceinline__ void kd_dma16(const void* src_lane, char* dst) {
-  const unsigned lds_addr = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src_lane), "s"(lds_addr)
-               : "memory");
-}
-
 // Groups [first, first + count) of sequence n.
 __device__ __forceinline__ void sequence_groups(const int32_t* soff, int n, int L, int& first, int& count) {
   const int lane = threadIdx.x & 63;
@@ -284,7 +271,7 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
       for (int i = 0; i < W_PER_WAVE; ++i) {
         const int fr = w * W_PER_WAVE + i;
-        kd_dma16(src + (size_t)fr * 1024 + 16 * lane, w_lds + b * WBYTES + fr * 1024);
+        lds_dma16(src + (size_t)fr * 1024 + 16 * lane, w_lds + b * WBYTES + fr * 1024);
       }
     }
   };
@@ -328,12 +315,12 @@ __device__ __forceinline__ void scan_body(const StateArgs& a, int unitg, int h, 
 #pragma unroll
       for (int i = 0; i < KD_PER_WAVE; ++i) {
         const int fr = w * KD_PER_WAVE + i;
-        kd_dma16(kg_src + (size_t)fr * 1024 + 16 * lane, kd_lds + fr * 1024);
+        lds_dma16(kg_src + (size_t)fr * 1024 + 16 * lane, kd_lds + fr * 1024);
       }
       if (w == 0) {
         const char* d_src = (const char*)(a.in.decay + unit * K);
 #pragma unroll
-        for (int i = 0; i < KD_DEC; ++i) kd_dma16(d_src + i * 1024 + 16 * lane, kd_lds + KD_FRAG * 1024 + i * 1024);
+        for (int i = 0; i < KD_DEC; ++i) lds_dma16(d_src + i * 1024 + 16 * lane, kd_lds + KD_FRAG * 1024 + i * 1024);
       }
     }
   };

@@ -4,7 +4,7 @@ its incoming state, the commit produces the final state.
 
 The WY kernel runs the 512 channels in two passes of the d = 256 layout, the
 scan carries 32-column state slices (plain scan, no two-level groups), and the
-reader takes 64-column state tiles.  Small cases compare with the fp64 token
+reader holds 16 state columns per wave in registers (read_wide_kernel).  Small cases compare with the fp64 token
 recurrence; the Flash-shaped workload (H=64, d=512) is checked on two heads
 against the fp64 chunked torch oracle.  d = 512 has no causal output: it is
 rejected with ValueError."""
