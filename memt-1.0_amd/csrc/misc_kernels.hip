@@ -99,10 +99,11 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 
 // ---------------------------------------------------------------------------
 // Snapshot reader for d = 256 and 512: read_fwd_kernel's product with the
-// state held in registers.  A workgroup of 8 waves takes 128 state columns of
-// one head (wave w: columns col0 + 16 w .. + 15) for a run of chunks.  Each wave
-// holds its 16 columns of bf16(S), all K channels (64 registers at d = 512), as
-// the A operand of o^T = bf16(S)^T q^T, loaded once per block, so the state is
+// state held in registers.  A workgroup takes 128 state columns of one head for
+// a run of chunks: 8 waves of 16 columns at d = 256, 4 waves of 32 at d = 512
+// (there each q operand read from LDS feeds two products).  Each wave holds its
+// columns of bf16(S), all K channels (128 registers at d = 512), as the A
+// operand of o^T = bf16(S)^T q^T, loaded once per block, so the state is
 // read from memory once per run instead of from LDS for every 16 tokens.  The
 // q rows come through LDS by direct loads in steps of a chunk (half a chunk at
 // d = 512, so that two workgroups share a CU and one covers the other's waits),
@@ -115,6 +116,9 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 constexpr int kWideCols = 128;  // state columns per wide-reader workgroup
 // rows of q per step: half a chunk at d = 512, so that two workgroups fit a CU's LDS
 __host__ __device__ constexpr int wide_rows(int K) { return K > 256 ? 32 : kChunk; }
+// waves per workgroup: at d = 512 four waves of 32 columns (two product tiles per q
+// operand read from LDS, 128 registers of state), at d = 256 eight of 16
+__host__ __device__ constexpr int wide_waves(int K) { return K > 256 ? 4 : 8; }
 template <int K>
 struct WideReadLds {
   static constexpr int TS = wide_rows(K);                        // token rows per step
@@ -132,7 +136,7 @@ __device__ __forceinline__ void vm_wait_barrier() {
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restrict__ q,
+__global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) / 2) void read_wide_kernel(const __bf16* __restrict__ q,
                                                         const float* __restrict__ snaps,
                                                         __bf16* __restrict__ o,
                                                         const int32_t* __restrict__ chunk_tok0,
@@ -141,7 +145,10 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
                                                         int n_units, int per, int H, float scale,
                                                         const int32_t* __restrict__ block_slot) {
   using L = WideReadLds<K>;
-  constexpr int NW = 8, NH = V / kWideCols, KS = K / 32, QSPR = L::QSPR, NSLOT = L::NSLOT;
+  constexpr int NW = wide_waves(K), CWN = kWideCols / (16 * NW);  // waves, 16-column tiles per wave
+  constexpr int NH = V / kWideCols, KS = K / 32, QSPR = L::QSPR, NSLOT = L::NSLOT;
+  constexpr int OPS = 16 / NW;  // direct loads per wave and state piece
+  static_assert(CWN == 1 || CWN == 2, "one or two column tiles per wave");
   constexpr int TS = L::TS, SPC = kChunk / TS, TT = TS / 16;  // rows per step, steps per chunk, token tiles
   static_assert(V % kWideCols == 0 && K == V && NSLOT >= 1 && NSLOT <= 4, "square heads of 256 or 512");
   __shared__ __attribute__((aligned(1024))) char q_lds[2 * L::BYTES];
@@ -155,7 +162,7 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
   const int c_end = __builtin_amdgcn_readfirstlane(min(c_begin + per, n_chunk));
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int colw = tile * kWideCols + 16 * w;  // this wave's first column
+  const int colw = tile * kWideCols + 16 * CWN * w;  // this wave's first column
 
   // step i (rows r0 .. r0 + TS - 1 of chunk c_begin + i / SPC, r0 = TS (i % SPC))
   // into buffer bi: the buffer is a flat run of 16-byte slots, row r's channels
@@ -183,7 +190,9 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
     }
   };
   // A operand of step s: element j is bf16(S)[32 s + 8 lg + j][colw + lr]
-  bf16x8 sr[KS];
+  // (two tiles: tile n, row 4 g + e is column 8 g + 4 n + e of the wave's 32, so
+  // that a lane ends with 8 adjacent columns of one token)
+  bf16x8 sr[KS][CWN];
   // The state reaches the registers through the free q buffer: rows
   // 32 p .. 32 p + 31 of the workgroup's 128 columns (16 KiB of fp32; one direct
   // load of 1 KiB covers two rows, 2 per wave) go to slot p % NSLOT, and each lane
@@ -194,14 +203,15 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
                       (size_t)(lane >> 5) * V + tile * kWideCols + 4 * (lane & 31);
     auto stage_piece = [&](int pc) {
 #pragma unroll
-      for (int i = 0; i < 16 / NW; ++i) {
+      for (int i = 0; i < OPS; ++i) {
         const int r2 = NW * i + w;  // rows 2 r2, 2 r2 + 1 of the piece
         lds_dma16(sp + (size_t)(32 * pc + 2 * r2) * V, free_buf + (pc % NSLOT) * L::PIECE + r2 * 1024);
       }
     };
-    // this lane's word of a piece: row 8 lg + j, column 16 w + lr
+    // this lane's word of a piece for tile n: row 8 lg + j, column colw - col0 + its column in the tile
+    const int lcol = CWN == 1 ? lr : 8 * (lr >> 2) + (lr & 3);
     const __attribute__((address_space(3))) char* const rb =
-        (const __attribute__((address_space(3))) char*)free_buf + (8 * lg * kWideCols + 16 * w + lr) * 4;
+        (const __attribute__((address_space(3))) char*)free_buf + (8 * lg * kWideCols + 16 * CWN * w + lcol) * 4;
 #pragma unroll
     for (int pc = 0; pc < NSLOT - 1 && pc < KS; ++pc) stage_piece(pc);
 #pragma unroll
@@ -209,14 +219,16 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
       if (pc + NSLOT - 1 < KS) stage_piece(pc + NSLOT - 1);
       // piece pc landed; the (2 per wave) loads of the pieces after it may still be in flight
       const int ahead = (KS - 1 - pc < NSLOT - 1) ? KS - 1 - pc : NSLOT - 1;
-      if (ahead >= 3) vm_wait_barrier<6>();
-      else if (ahead == 2) vm_wait_barrier<4>();
-      else if (ahead == 1) vm_wait_barrier<2>();
+      if (ahead >= 3) vm_wait_barrier<3 * OPS>();
+      else if (ahead == 2) vm_wait_barrier<2 * OPS>();
+      else if (ahead == 1) vm_wait_barrier<OPS>();
       else vm_wait_barrier<0>();
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        sr[pc][j] = (__bf16)*(const __attribute__((address_space(3))) float*)(rb + (pc % NSLOT) * L::PIECE +
-                                                                              j * kWideCols * 4);
+#pragma unroll
+        for (int n = 0; n < CWN; ++n)
+          sr[pc][n][j] = (__bf16)*(const __attribute__((address_space(3))) float*)(
+              rb + (pc % NSLOT) * L::PIECE + j * kWideCols * 4 + 16 * n);
       // every wave's reads of the slot done before a later piece lands there
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
@@ -239,9 +251,11 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
     }
     // the next step's rows into the other buffer
     if (i + 1 < n_steps) stage(i + 1, bi ^ 1);
-    f32x4 acc[TT];
+    f32x4 acc[TT][CWN];
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) acc[tt] = zero4();
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int n = 0; n < CWN; ++n) acc[tt][n] = zero4();
     if (len > 0) {
       // this lane's q operand: token 16 tt + lr, channels 32 s + 8 lg .. + 7 (its
       // offset formed here from an opaque lane index: a value kept across the
@@ -256,7 +270,8 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
           const bf16x8 qv = *(const __attribute__((address_space(3))) bf16x8*)(qb + (16 * tt * QSPR + 4 * s) * 16);
-          acc[tt] = mfma_bf16(sr[s], qv, acc[tt]);
+#pragma unroll
+          for (int n = 0; n < CWN; ++n) acc[tt][n] = mfma_bf16(sr[s][n], qv, acc[tt][n]);
         }
     }
     // every wave's loads of the next step landed, every wave done with this buffer
@@ -265,15 +280,25 @@ __global__ __launch_bounds__(512, 4) void read_wide_kernel(const __bf16* __restr
     if (len > 0) {
       int sl = lane;  // opaque again: the row offsets are formed here
       asm volatile("" : "+v"(sl));
-      __bf16* const op = o + ((size_t)tok0 * H + h) * V + colw + 4 * (sl >> 4);
+      __bf16* const op = o + ((size_t)tok0 * H + h) * V + colw + 4 * CWN * (sl >> 4);
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         const int t = 16 * tt + (sl & 15);
         if (t < len) {
-          bf16x4 v;
+          if constexpr (CWN == 1) {
+            bf16x4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (__bf16)(acc[tt][e] * scale);
-          *(bf16x4*)(op + (size_t)t * H * V) = v;
+            for (int e = 0; e < 4; ++e) v[e] = (__bf16)(acc[tt][0][e] * scale);
+            *(bf16x4*)(op + (size_t)t * H * V) = v;
+          } else {
+            bf16x8 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = (__bf16)(acc[tt][0][e] * scale);
+              v[4 + e] = (__bf16)(acc[tt][1][e] * scale);
+            }
+            *(bf16x8*)(op + (size_t)t * H * V) = v;
+          }
         }
       }
     }
@@ -586,10 +611,10 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
     const int n_units = (n_chunk + per - 1) / per * H;
     const int n_blocks = (n_units + 7) / 8 * 8 * nh;
     if (K == 256)
-      hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(512), 0, stream, q, snaps, o,
+      hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(64 * wide_waves(256)), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     else
-      hipLaunchKernelGGL((read_wide_kernel<512, 512>), dim3(n_blocks), dim3(512), 0, stream, q, snaps, o,
+      hipLaunchKernelGGL((read_wide_kernel<512, 512>), dim3(n_blocks), dim3(64 * wide_waves(512)), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     return hipGetLastError();
   }
