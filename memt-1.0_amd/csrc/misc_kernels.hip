@@ -1,11 +1,13 @@
 // Readout, normalisation and layout kernels of the GDN-2 memory path.
 #include "gdn2_internal.h"
 
+#include <algorithm>
+
 namespace memt {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Snapshot reader (models/qwen/ops/_triton/read.py:22-71) for d <= 128: per
+// Snapshot reader (models/qwen/ops/_triton/read.py:22-71) for d = 64: per
 // (chunk, head), o[t] = bf16(scale * q[t] . bf16(S_block)), bf16 MFMA, fp32
 // accumulation.  A workgroup takes all V state columns of one head for a run of
 // kReadRun consecutive chunks, and reloads the bf16 state tile only when the
@@ -16,6 +18,7 @@ namespace {
 // chunks per reader workgroup (snapshot mode at 16 heads, 8192 tokens, d = 128:
 // runs of 1, 2, 8 or 16 chunks measured 2-17 % slower than 4)
 constexpr int kReadRun = 4;
+constexpr int kWideCols = 128;  // state columns per read_wide_kernel workgroup (heads this wide read there)
 
 template <int K, int V>
 __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict__ q,
@@ -25,7 +28,7 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
                                                        int n_chunk, int n_units, int H, float scale,
                                                        const int32_t* block_slot) {
   constexpr int CB = V, SKP = K + 8, per = kReadRun;
-  static_assert(V <= 128, "d > 128 reads in read_wide_kernel");
+  static_assert(V < kWideCols, "d >= 128 reads in read_wide_kernel");
   __shared__ __attribute__((aligned(16))) __bf16 S_lds[CB * SKP];  // column-major bf16(S)
   const int unit = blockIdx.x;  // (run, head)
   if (unit >= n_units) return;
@@ -98,9 +101,9 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Snapshot reader for d = 256 and 512: read_fwd_kernel's product with the
+// Snapshot reader for d = 128, 256 and 512: read_fwd_kernel's product with the
 // state held in registers.  A workgroup takes 128 state columns of one head for
-// a run of chunks: 8 waves of 16 columns at d = 256, 4 waves of 32 at d = 512
+// a run of chunks: 8 waves of 16 columns up to d = 256, 4 waves of 32 at d = 512
 // (there each q operand read from LDS feeds two products).  Each wave holds its
 // columns of bf16(S), all K channels (128 registers at d = 512), as the A
 // operand of o^T = bf16(S)^T q^T, loaded once per block, so the state is
@@ -113,12 +116,13 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 // one (run, head) read the same q rows; their block indices are 8 apart, so they
 // share an XCD and its L2 (HBM fetches at d = 512: q and the state once).
 // ---------------------------------------------------------------------------
-constexpr int kWideCols = 128;  // state columns per wide-reader workgroup
 // rows of q per step: half a chunk at d = 512, so that two workgroups fit a CU's LDS
 __host__ __device__ constexpr int wide_rows(int K) { return K > 256 ? 32 : kChunk; }
 // waves per workgroup: at d = 512 four waves of 32 columns (two product tiles per q
 // operand read from LDS, 128 registers of state), at d = 256 eight of 16
 __host__ __device__ constexpr int wide_waves(int K) { return K > 256 ? 4 : 8; }
+// workgroups per CU: two at d >= 256 (66 KB of LDS each), four at d = 128 (34 KB)
+__host__ __device__ constexpr int wide_per_cu(int K) { return K > 128 ? 2 : 4; }
 template <int K>
 struct WideReadLds {
   static constexpr int TS = wide_rows(K);                        // token rows per step
@@ -136,7 +140,7 @@ __device__ __forceinline__ void vm_wait_barrier() {
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) / 2) void read_wide_kernel(const __bf16* __restrict__ q,
+__global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) / 4) void read_wide_kernel(const __bf16* __restrict__ q,
                                                         const float* __restrict__ snaps,
                                                         __bf16* __restrict__ o,
                                                         const int32_t* __restrict__ chunk_tok0,
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) / 2) void read_wi
   constexpr int OPS = 16 / NW;  // direct loads per wave and state piece
   static_assert(CWN == 1 || CWN == 2, "one or two column tiles per wave");
   constexpr int TS = L::TS, SPC = kChunk / TS, TT = TS / 16;  // rows per step, steps per chunk, token tiles
-  static_assert(V % kWideCols == 0 && K == V && NSLOT >= 1 && NSLOT <= 4, "square heads of 256 or 512");
+  static_assert(V % kWideCols == 0 && K == V && NSLOT >= 1 && NSLOT <= 4, "square heads of 128, 256 or 512");
   __shared__ __attribute__((aligned(1024))) char q_lds[2 * L::BYTES];
   // block b -> column tile (b / 8) % NH of unit (b % 8) + 8 (b / (8 NH)); a unit is (run, head)
   const int b = blockIdx.x;
@@ -601,16 +605,20 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
     return hipGetLastError();                                                                                  \
   }
   MEMT_RD(64, 64)
-  MEMT_RD(128, 128)
 #undef MEMT_RD
-  if (K == V && (K == 256 || K == 512)) {
-    // runs sized so the grid fills the chip once, two workgroups per CU (66 KB of LDS each)
-    const int nh = V / kWideCols, per_run = H * nh, slots = device_cus() * 2;
+  if (K == V && (K == 128 || K == 256 || K == 512)) {
+    // runs sized so the grid fills the chip once
+    const int nh = V / kWideCols, per_run = H * nh, slots = device_cus() * wide_per_cu(K);
     const int runs_wanted = (slots + per_run - 1) / per_run;  // at least 1
-    const int per = (n_chunk + runs_wanted - 1) / runs_wanted;
+    // (at d = 128 a run's state, 64 KB, is two chunks' q and o: runs of at least
+    // kReadRun chunks keep the state reloads to a third of the traffic)
+    const int per = std::max((n_chunk + runs_wanted - 1) / runs_wanted, K == 128 ? kReadRun : 1);
     const int n_units = (n_chunk + per - 1) / per * H;
     const int n_blocks = (n_units + 7) / 8 * 8 * nh;
-    if (K == 256)
+    if (K == 128)
+      hipLaunchKernelGGL((read_wide_kernel<128, 128>), dim3(n_blocks), dim3(64 * wide_waves(128)), 0, stream, q, snaps, o,
+                         chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
+    else if (K == 256)
       hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(64 * wide_waves(256)), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     else

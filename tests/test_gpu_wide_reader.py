@@ -1,4 +1,4 @@
-"""GPU parity of the d = 256 / 512 snapshot reader (read_wide_kernel), the
+"""GPU parity of the d = 128 / 256 / 512 snapshot reader (read_wide_kernel), the
 reader of models/qwen/ops/read.py:10-39 and models/deepseek/ops/read.py:6-31:
 every token reads bf16(scale * q . bf16(S_block)).
 
@@ -27,7 +27,7 @@ def _q(rng, T, H, D):
     return O.bf16_round(O.l2norm(rng.standard_normal((1, T, H, D)).astype(np.float32))[0])
 
 
-@pytest.mark.parametrize("D", [256, 512])
+@pytest.mark.parametrize("D", [128, 256, 512])
 @pytest.mark.parametrize("H,lengths", [(3, [130, 1, 2000, 64, 63, 65]), (64, [40, 64, 1])])
 def test_wide_reader_ragged_samples(dev, D, H, lengths):
     print(f"wide reader D={D} H={H} lengths={lengths}", flush=True)
@@ -40,7 +40,7 @@ def test_wide_reader_ragged_samples(dev, D, H, lengths):
     assert O.parity_err(host(out), ref, out_bf16=True) <= TOL
 
 
-@pytest.mark.parametrize("D", [256, 512])
+@pytest.mark.parametrize("D", [128, 256, 512])
 def test_wide_reader_block_changes_inside_a_run(dev, D):
     """Read blocks inside one sample: a workgroup's run of chunks crosses block
     boundaries (one of them a single token), and the state is reloaded there."""
@@ -63,7 +63,7 @@ def test_wide_reader_block_changes_inside_a_run(dev, D):
     assert O.parity_err(host(out)[0], ref, out_bf16=True) <= TOL
 
 
-@pytest.mark.parametrize("D", [256, 512])
+@pytest.mark.parametrize("D", [128, 256, 512])
 def test_wide_reader_pool_slots(dev, D):
     """The pool read in place: sample n reads pool[slots[n]]."""
     H, lengths = 4, [1000, 5, 995]
