@@ -103,9 +103,9 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 // ---------------------------------------------------------------------------
 // Snapshot reader for d = 128, 256 and 512: read_fwd_kernel's product with the
 // state held in registers.  A workgroup takes 128 state columns of one head for
-// a run of chunks: 8 waves of 16 columns up to d = 256, 4 waves of 32 at d = 512
-// (there each q operand read from LDS feeds two products).  Each wave holds its
-// columns of bf16(S), all K channels (128 registers at d = 512), as the A
+// a run of chunks, 4 waves of 32 columns (each q operand read from LDS feeds two
+// products).  Each wave holds its columns of bf16(S), all K channels (128
+// registers at d = 512), as the A
 // operand of o^T = bf16(S)^T q^T, loaded once per block, so the state is
 // read from memory once per run instead of from LDS for every 16 tokens.  The
 // q rows come through LDS by direct loads in steps of a chunk (half a chunk at
@@ -118,9 +118,11 @@ __global__ __launch_bounds__(256) void read_fwd_kernel(const __bf16* __restrict_
 // ---------------------------------------------------------------------------
 // rows of q per step: half a chunk at d = 512, so that two workgroups fit a CU's LDS
 __host__ __device__ constexpr int wide_rows(int K) { return K > 256 ? 32 : kChunk; }
-// waves per workgroup: at d = 512 four waves of 32 columns (two product tiles per q
-// operand read from LDS, 128 registers of state), at d = 256 eight of 16
-__host__ __device__ constexpr int wide_waves(int K) { return K > 256 ? 4 : 8; }
+// waves per workgroup: four of 32 columns, two product tiles per q operand read
+// from LDS (128 registers of state at d = 512).  Against eight waves of 16 columns:
+// 0.42 -> 0.37 ms at d = 512 (64 heads, 8192 tokens), 0.30 -> 0.23 ms at d = 256
+// (64 heads, 16384 tokens), 19.5 -> 16.3 us at d = 128 (16 heads, 8192 tokens)
+constexpr int kWideWaves = 4;
 // workgroups per CU: two at d >= 256 (66 KB of LDS each), four at d = 128 (34 KB)
 __host__ __device__ constexpr int wide_per_cu(int K) { return K > 128 ? 2 : 4; }
 template <int K>
@@ -140,7 +142,7 @@ __device__ __forceinline__ void vm_wait_barrier() {
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) / 4) void read_wide_kernel(const __bf16* __restrict__ q,
+__global__ __launch_bounds__(64 * kWideWaves, kWideWaves * wide_per_cu(K) / 4) void read_wide_kernel(const __bf16* __restrict__ q,
                                                         const float* __restrict__ snaps,
                                                         __bf16* __restrict__ o,
                                                         const int32_t* __restrict__ chunk_tok0,
@@ -149,10 +151,10 @@ __global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) 
                                                         int n_units, int per, int H, float scale,
                                                         const int32_t* __restrict__ block_slot) {
   using L = WideReadLds<K>;
-  constexpr int NW = wide_waves(K), CWN = kWideCols / (16 * NW);  // waves, 16-column tiles per wave
+  constexpr int NW = kWideWaves, CWN = kWideCols / (16 * NW);  // waves, 16-column tiles per wave
   constexpr int NH = V / kWideCols, KS = K / 32, QSPR = L::QSPR, NSLOT = L::NSLOT;
   constexpr int OPS = 16 / NW;  // direct loads per wave and state piece
-  static_assert(CWN == 1 || CWN == 2, "one or two column tiles per wave");
+  static_assert(CWN == 2, "two column tiles per wave");
   constexpr int TS = L::TS, SPC = kChunk / TS, TT = TS / 16;  // rows per step, steps per chunk, token tiles
   static_assert(V % kWideCols == 0 && K == V && NSLOT >= 1 && NSLOT <= 4, "square heads of 128, 256 or 512");
   __shared__ __attribute__((aligned(1024))) char q_lds[2 * L::BYTES];
@@ -193,9 +195,10 @@ __global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) 
       }
     }
   };
-  // A operand of step s: element j is bf16(S)[32 s + 8 lg + j][colw + lr]
-  // (two tiles: tile n, row 4 g + e is column 8 g + 4 n + e of the wave's 32, so
-  // that a lane ends with 8 adjacent columns of one token)
+  // A operand of step s, tile n: element j is
+  // bf16(S)[32 s + 8 lg + j][colw + 8 (lr / 4) + 4 n + lr % 4] (row 4 g + e of tile n
+  // is column 8 g + 4 n + e of the wave's 32, so that a lane ends with 8 adjacent
+  // columns of one token)
   bf16x8 sr[KS][CWN];
   // The state reaches the registers through the free q buffer: rows
   // 32 p .. 32 p + 31 of the workgroup's 128 columns (16 KiB of fp32; one direct
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) 
       }
     };
     // this lane's word of a piece for tile n: row 8 lg + j, column colw - col0 + its column in the tile
-    const int lcol = CWN == 1 ? lr : 8 * (lr >> 2) + (lr & 3);
+    const int lcol = 8 * (lr >> 2) + (lr & 3);
     const __attribute__((address_space(3))) char* const rb =
         (const __attribute__((address_space(3))) char*)free_buf + (8 * lg * kWideCols + 16 * CWN * w + lcol) * 4;
 #pragma unroll
@@ -289,20 +292,13 @@ __global__ __launch_bounds__(64 * wide_waves(K), wide_waves(K) * wide_per_cu(K) 
       for (int tt = 0; tt < TT; ++tt) {
         const int t = 16 * tt + (sl & 15);
         if (t < len) {
-          if constexpr (CWN == 1) {
-            bf16x4 v;
+          bf16x8 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (__bf16)(acc[tt][0][e] * scale);
-            *(bf16x4*)(op + (size_t)t * H * V) = v;
-          } else {
-            bf16x8 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = (__bf16)(acc[tt][0][e] * scale);
-              v[4 + e] = (__bf16)(acc[tt][1][e] * scale);
-            }
-            *(bf16x8*)(op + (size_t)t * H * V) = v;
+          for (int e = 0; e < 4; ++e) {
+            v[e] = (__bf16)(acc[tt][0][e] * scale);
+            v[4 + e] = (__bf16)(acc[tt][1][e] * scale);
           }
+          *(bf16x8*)(op + (size_t)t * H * V) = v;
         }
       }
     }
@@ -616,13 +612,13 @@ hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const
     const int n_units = (n_chunk + per - 1) / per * H;
     const int n_blocks = (n_units + 7) / 8 * 8 * nh;
     if (K == 128)
-      hipLaunchKernelGGL((read_wide_kernel<128, 128>), dim3(n_blocks), dim3(64 * wide_waves(128)), 0, stream, q, snaps, o,
+      hipLaunchKernelGGL((read_wide_kernel<128, 128>), dim3(n_blocks), dim3(64 * kWideWaves), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     else if (K == 256)
-      hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(64 * wide_waves(256)), 0, stream, q, snaps, o,
+      hipLaunchKernelGGL((read_wide_kernel<256, 256>), dim3(n_blocks), dim3(64 * kWideWaves), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     else
-      hipLaunchKernelGGL((read_wide_kernel<512, 512>), dim3(n_blocks), dim3(64 * wide_waves(512)), 0, stream, q, snaps, o,
+      hipLaunchKernelGGL((read_wide_kernel<512, 512>), dim3(n_blocks), dim3(64 * kWideWaves), 0, stream, q, snaps, o,
                          chunk_tok0, chunk_len, chunk_block_ids, n_chunk, n_units, per, H, scale, block_slot);
     return hipGetLastError();
   }
