@@ -2,6 +2,7 @@
 #include "gdn2_internal.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace memt {
 namespace {
@@ -577,16 +578,18 @@ __global__ __launch_bounds__(256) void wy_import_kernel(const __bf16* w, const _
 
 }  // namespace
 
-// CUs of the current device, looked up once per device
+// CUs of the current device, looked up once per device (callers on several host
+// threads may race to fill an entry; they store the same value)
 static int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 hipError_t launch_read_fwd(const __bf16* q, const float* snaps, __bf16* o, const int32_t* chunk_tok0,
