@@ -273,14 +273,27 @@ __global__ __launch_bounds__(64 * kWideWaves, kWideWaves * wide_per_cu(K) / 4) v
       asm volatile("" : "+v"(ml));
       const __attribute__((address_space(3))) char* const qb =
           (const __attribute__((address_space(3))) char*)q_lds + bi * L::BYTES + ((ml & 15) * QSPR + (ml >> 4)) * 16;
+      // the operands in batches of 8 reads, all issued before the batch's products
+      // (left to itself the compiler waited for each read before its two products;
+      // 0.36 -> 0.34 ms at d = 512, 64 heads and 8192 tokens)
+      constexpr int SB = 8 / TT;  // channel steps per batch
+      static_assert(KS % SB == 0, "channel steps in whole batches");
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+      for (int s0 = 0; s0 < KS; s0 += SB) {
+        bf16x8 qv[SB][TT];
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
-          const bf16x8 qv = *(const __attribute__((address_space(3))) bf16x8*)(qb + (16 * tt * QSPR + 4 * s) * 16);
+        for (int ds = 0; ds < SB; ++ds)
 #pragma unroll
-          for (int n = 0; n < CWN; ++n) acc[tt][n] = mfma_bf16(sr[s][n], qv, acc[tt][n]);
-        }
+          for (int tt = 0; tt < TT; ++tt)
+            qv[ds][tt] = *(const __attribute__((address_space(3))) bf16x8*)(qb + (16 * tt * QSPR + 4 * (s0 + ds)) * 16);
+        __builtin_amdgcn_sched_barrier(0);  // keep the batch's reads together
+#pragma unroll
+        for (int ds = 0; ds < SB; ++ds)
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int n = 0; n < CWN; ++n) acc[tt][n] = mfma_bf16(sr[s0 + ds][n], qv[ds][tt], acc[tt][n]);
+      }
     }
     // every wave's loads of the next step landed, every wave done with this buffer
     // (the wait also covers the previous step's stores, long since issued)
